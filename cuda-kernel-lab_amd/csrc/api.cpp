@@ -1,0 +1,754 @@
+// api.cpp -- C ABI of libpdattn: validation, planning, workspace handling, launch sequencing.
+//
+// Host side of the decode-attention path of qilem/cuda-kernel-lab (01_decode_attention.cu),
+// re-designed for one MI355X: planners size grids from the runtime's occupancy query and the CU
+// count, errors are returned as status codes, and workspaces are either caller-provided (never
+// reallocated) or library-owned (grown like the reference's Workspace).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/pdattn.h"
+#include "pdattn_internal.h"
+
+using namespace pdattn;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return status;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(PDATTN_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define PD_HIP(call)                                              \
+    do {                                                          \
+        hipError_t e_ = (call);                                   \
+        if (e_ != hipSuccess) return hip_fail(e_, #call);         \
+    } while (0)
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool valid_group(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
+
+// Per-device facts cached on first use: CU count, arch name, kernel occupancies.
+struct DeviceFacts {
+    int cus = 0;
+    int occ_partial[9] = {};
+    int occ_streamk[9] = {};
+    int occ_prefix[9] = {};
+    char arch[64] = {};
+};
+
+std::mutex g_dev_mu;
+std::vector<DeviceFacts> g_dev;
+
+int device_facts(DeviceFacts* out) {
+    int dev = 0;
+    PD_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_dev_mu);
+    if ((int)g_dev.size() <= dev) g_dev.resize(dev + 1);
+    DeviceFacts& f = g_dev[dev];
+    if (f.cus == 0) {
+        hipDeviceProp_t prop;
+        PD_HIP(hipGetDeviceProperties(&prop, dev));
+        f.cus = prop.multiProcessorCount;
+        snprintf(f.arch, sizeof f.arch, "%s", prop.gcnArchName);
+        for (int G : {1, 2, 4, 8}) {
+            f.occ_partial[G] = occupancy_decode_partial(G);
+            f.occ_streamk[G] = occupancy_decode_streamk(G);
+            f.occ_prefix[G] = occupancy_cascade_prefix(G);
+        }
+    }
+    *out = f;
+    return PDATTN_OK;
+}
+
+int check_heads(int Hq, int Hkv, int* G) {
+    if (Hq <= 0 || Hkv <= 0) return fail(PDATTN_ERR_INVALID_ARGUMENT, "Hq=%d Hkv=%d must be positive", Hq, Hkv);
+    if (Hq % Hkv) return fail(PDATTN_ERR_UNSUPPORTED, "Hq=%d is not a multiple of Hkv=%d", Hq, Hkv);
+    *G = Hq / Hkv;
+    if (!valid_group(*G)) return fail(PDATTN_ERR_UNSUPPORTED, "GQA group size %d not in {1,2,4,8}", *G);
+    return PDATTN_OK;
+}
+
+// Host page table check: indptr monotone from 0..nnz, last_page_len in [1,16] for non-empty.
+int check_host_table(const int32_t* indptr, const int32_t* last, int B) {
+    if (!indptr || (B > 0 && !last)) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null host page table");
+    if (indptr[0] < 0) return fail(PDATTN_ERR_PAGE_TABLE, "kv_indptr[0]=%d is negative", indptr[0]);
+    for (int b = 0; b < B; ++b) {
+        if (indptr[b + 1] < indptr[b])
+            return fail(PDATTN_ERR_PAGE_TABLE, "kv_indptr not monotone at %d (%d > %d)", b, indptr[b], indptr[b + 1]);
+        if (indptr[b + 1] > indptr[b] && (last[b] < 1 || last[b] > kPage))
+            return fail(PDATTN_ERR_PAGE_TABLE, "kv_last_page_len[%d]=%d outside [1,16]", b, last[b]);
+    }
+    return PDATTN_OK;
+}
+
+int check_decode_params(const pdattn_decode_params* p, int G) {
+    if (!p) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null params");
+    if (p->B < 0) return fail(PDATTN_ERR_INVALID_ARGUMENT, "B=%d is negative", p->B);
+    int g = 0;
+    if (int st = check_heads(p->Hq, p->Hkv, &g)) return st;
+    if (g != G) return fail(PDATTN_ERR_INVALID_ARGUMENT, "G=%d but Hq/Hkv=%d", G, g);
+    if (p->B == 0) return PDATTN_OK;
+    if (!p->q || !p->k_cache || !p->v_cache || !p->kv_indptr || !p->kv_indices || !p->kv_last_page_len)
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "null device pointer in params");
+    if (!aligned16(p->q) || !aligned16(p->k_cache) || !aligned16(p->v_cache))
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "q / k_cache / v_cache must be 16-byte aligned");
+    if (p->num_chunks < 1 || p->chunk_tokens < 1)
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "num_chunks=%d chunk_tokens=%d must be >= 1", p->num_chunks, p->chunk_tokens);
+    if (p->kv_start < 0 || p->chunk_base < 0)
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "kv_start / chunk_base must be >= 0");
+    if (p->part_stride < p->chunk_base + p->num_chunks)
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "part_stride=%d < chunk_base + num_chunks=%d",
+                    p->part_stride, p->chunk_base + p->num_chunks);
+    if (!std::isfinite(p->sm_scale)) return fail(PDATTN_ERR_INVALID_ARGUMENT, "sm_scale is not finite");
+    return PDATTN_OK;
+}
+
+PartialArgs to_partial_args(const pdattn_decode_params* p) {
+    PartialArgs a;
+    a.q = static_cast<const _Float16*>(p->q);
+    a.k = static_cast<const uint8_t*>(p->k_cache);
+    a.v = static_cast<const uint8_t*>(p->v_cache);
+    a.kv_indptr = p->kv_indptr;
+    a.kv_indices = p->kv_indices;
+    a.kv_last = p->kv_last_page_len;
+    a.part_o = p->part_o;
+    a.part_lse = p->part_lse;
+    a.B = p->B;
+    a.Hq = p->Hq;
+    a.Hkv = p->Hkv;
+    a.num_chunks = p->num_chunks;
+    a.chunk_tokens = p->chunk_tokens;
+    a.kv_start = p->kv_start;
+    a.chunk_base = p->chunk_base;
+    a.part_stride = p->part_stride;
+    a.scale_log2 = p->sm_scale * 1.4426950408889634f;
+    return a;
+}
+
+int ensure_ws(pdattn_workspace* ws, size_t need) {
+    if (!ws) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null workspace");
+    if (ws->bytes >= need && ws->base) return PDATTN_OK;
+    if (ws->base && !ws->owned)
+        return fail(PDATTN_ERR_WORKSPACE, "caller-provided workspace holds %zu bytes, %zu needed", ws->bytes, need);
+    return pdattn_workspace_reserve(ws, need);
+}
+
+}  // namespace
+
+// ---- plans ------------------------------------------------------------------------------------
+
+struct pdattn_plan {
+    int B = 0, Hq = 0, Hkv = 0, G = 0;
+    int nnz = 0, jbase = 0, W = 1, n_empty = 0, b_first = 0;
+    int64_t U = 0;
+    int split_pairs = 0, max_contrib = 0;
+    // workspace layout (bytes from the base)
+    size_t off_desc = 0, off_empty = 0, off_cnt = 0, off_plse = 0, off_po = 0, ws_bytes = 0;
+    std::vector<int32_t> host_blob;   // desc_b0[W] followed by empty_seq[n_empty]
+    void* pinned = nullptr;           // pinned copy of host_blob for stream-ordered upload
+    size_t blob_bytes = 0;
+    const void* uploaded_to = nullptr;
+};
+
+struct pdattn_cascade_plan {
+    int use = 0;
+    int P = 0, Lp = 0;                 // shared pages / tokens
+    int cpre = 0, ctok = 0, qgroups = 0;
+    pdattn_decode_params base{};
+    const int32_t* d_prefix_pages = nullptr;
+    pdattn_plan sk;                    // balanced plan of the suffix (or of the whole batch)
+    std::vector<int32_t> tbl;          // suffix indptr [B+1] then suffix indices [nnz_s]
+    void* pinned = nullptr;
+    size_t off_ppo = 0, off_pplse = 0, off_tbl = 0, off_sk = 0, ws_bytes = 0;
+    const void* uploaded_to = nullptr;
+};
+
+namespace {
+
+// Balanced split of the flattened (kv head, page) units over W workgroups; see pdattn.h.
+int build_streamk_plan(const int32_t* indptr, const int32_t* last, int B, int Hq, int Hkv,
+                       int force_wg, pdattn_plan* pl) {
+    int G = 0;
+    if (int st = check_heads(Hq, Hkv, &G)) return st;
+    if (B < 0) return fail(PDATTN_ERR_INVALID_ARGUMENT, "B=%d is negative", B);
+    if (B > 0)
+        if (int st = check_host_table(indptr, last, B)) return st;
+
+    pl->B = B;
+    pl->Hq = Hq;
+    pl->Hkv = Hkv;
+    pl->G = G;
+    pl->jbase = B > 0 ? indptr[0] : 0;
+    pl->nnz = B > 0 ? indptr[B] - indptr[0] : 0;
+    pl->U = (int64_t)Hkv * pl->nnz;
+    std::vector<int32_t> empty;
+    pl->b_first = -1;
+    for (int b = 0; b < B; ++b) {
+        if (indptr[b + 1] == indptr[b]) empty.push_back(b);
+        else if (pl->b_first < 0) pl->b_first = b;
+    }
+    if (pl->b_first < 0) pl->b_first = 0;
+    pl->n_empty = (int)empty.size();
+
+    // grid: one full wave of resident workgroups (runtime occupancy x CUs), never more
+    // workgroups than page units; a forced size needs no device query
+    int64_t W = force_wg;
+    if (W <= 0) {
+        DeviceFacts f;
+        if (int st = device_facts(&f)) return st;
+        W = (int64_t)f.cus * std::max(1, f.occ_streamk[G]);
+        if (pl->U == 0) W = std::min<int64_t>(W, f.cus);
+    }
+    if (pl->U == 0) W = std::max<int64_t>(1, std::min<int64_t>(W, (int64_t)pl->n_empty * Hq));
+    else W = std::max<int64_t>(1, std::min<int64_t>(W, pl->U));
+    if (W > (1 << 30)) return fail(PDATTN_ERR_INVALID_ARGUMENT, "grid too large");
+    pl->W = (int)W;
+
+    // desc_b0[w]: the sequence holding the first page of workgroup w's range
+    std::vector<int32_t> desc(pl->W, 0);
+    if (pl->U > 0) {
+        for (int w = 0; w < pl->W; ++w) {
+            const int64_t u0 = pl->U * w / pl->W;
+            const int j = (int)(u0 % pl->nnz);
+            // first b with indptr[b+1] - jbase > j
+            const int32_t* it = std::upper_bound(indptr + 1, indptr + B + 1, j + pl->jbase);
+            desc[w] = (int)(it - (indptr + 1));
+        }
+        // contributor statistics
+        int split = 0, mx = 1;
+        for (int kvh = 0; kvh < Hkv; ++kvh)
+            for (int b = 0; b < B; ++b) {
+                const int pb = indptr[b] - pl->jbase, pe = indptr[b + 1] - pl->jbase;
+                if (pe == pb) continue;
+                const int64_t uf = (int64_t)kvh * pl->nnz + pb, ul = (int64_t)kvh * pl->nnz + pe - 1;
+                const int64_t w1 = ((uf + 1) * pl->W - 1) / pl->U, w2 = ((ul + 1) * pl->W - 1) / pl->U;
+                if (w2 > w1) ++split;
+                mx = std::max<int>(mx, (int)(w2 - w1 + 1));
+            }
+        pl->split_pairs = split;
+        pl->max_contrib = mx;
+    }
+    pl->host_blob = desc;
+    pl->host_blob.insert(pl->host_blob.end(), empty.begin(), empty.end());
+
+    const size_t pairs = (size_t)B * Hkv;
+    const size_t slots = pairs + (size_t)pl->W;
+    size_t off = 0;
+    pl->off_desc = off;  off += align_up(sizeof(int32_t) * pl->W);
+    pl->off_empty = off; off += align_up(sizeof(int32_t) * std::max(1, pl->n_empty));
+    pl->off_cnt = off;   off += align_up(sizeof(int32_t) * std::max<size_t>(1, pairs));
+    pl->off_plse = off;  off += align_up(sizeof(float) * slots * G);
+    pl->off_po = off;    off += align_up(sizeof(float) * slots * G * kHeadDim);
+    pl->ws_bytes = off;
+
+    pl->blob_bytes = sizeof(int32_t) * pl->host_blob.size();
+    return PDATTN_OK;
+}
+
+void free_plan_storage(pdattn_plan* pl) {
+    if (pl && pl->pinned) {
+        (void)hipHostFree(pl->pinned);
+        pl->pinned = nullptr;
+    }
+}
+
+int upload_streamk(pdattn_plan* pl, void* ws, size_t bytes, hipStream_t s) {
+    if (!ws) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null workspace");
+    if (bytes < pl->ws_bytes)
+        return fail(PDATTN_ERR_WORKSPACE, "workspace holds %zu bytes, plan needs %zu", bytes, pl->ws_bytes);
+    char* base = static_cast<char*>(ws);
+    const size_t desc_bytes = sizeof(int32_t) * pl->W;
+    if (pl->blob_bytes && !pl->pinned) {
+        // pinned staging copy, made once: the copy below is stream-ordered and asynchronous
+        hipError_t e = hipHostMalloc(&pl->pinned, pl->blob_bytes, hipHostMallocDefault);
+        if (e != hipSuccess) return hip_fail(e, "hipHostMalloc(plan)");
+        std::memcpy(pl->pinned, pl->host_blob.data(), pl->blob_bytes);
+    }
+    if (pl->blob_bytes) {
+        PD_HIP(hipMemcpyAsync(base + pl->off_desc, pl->pinned, desc_bytes, hipMemcpyHostToDevice, s));
+        if (pl->n_empty)
+            PD_HIP(hipMemcpyAsync(base + pl->off_empty, static_cast<char*>(pl->pinned) + desc_bytes,
+                                  sizeof(int32_t) * pl->n_empty, hipMemcpyHostToDevice, s));
+    }
+    const size_t pairs = (size_t)pl->B * pl->Hkv;
+    PD_HIP(launch_fill_i32(reinterpret_cast<int32_t*>(base + pl->off_cnt), 0, std::max<size_t>(1, pairs), s));
+    pl->uploaded_to = ws;
+    return PDATTN_OK;
+}
+
+int run_streamk(const pdattn_plan* pl, const void* q, const void* k, const void* v,
+                const int32_t* indptr, const int32_t* indices, const int32_t* last, float sm_scale,
+                void* out, float* lse, void* ws, size_t bytes, hipStream_t s,
+                const float* extra_o = nullptr, const float* extra_lse = nullptr, int n_extra = 0) {
+    if (ws != pl->uploaded_to)
+        return fail(PDATTN_ERR_NOT_READY, "plan was not uploaded into this workspace");
+    if (bytes < pl->ws_bytes)
+        return fail(PDATTN_ERR_WORKSPACE, "workspace holds %zu bytes, plan needs %zu", bytes, pl->ws_bytes);
+    if (pl->B == 0) return PDATTN_OK;
+    if (!out || !lse || !q || !indptr || !last || (pl->U > 0 && (!k || !v || !indices)))
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "null device pointer");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "q / k_cache / v_cache / out must be 16-byte aligned");
+    if (!std::isfinite(sm_scale)) return fail(PDATTN_ERR_INVALID_ARGUMENT, "sm_scale is not finite");
+    char* base = static_cast<char*>(ws);
+    StreamKArgs a;
+    a.q = static_cast<const _Float16*>(q);
+    a.k = static_cast<const uint8_t*>(k);
+    a.v = static_cast<const uint8_t*>(v);
+    a.kv_indptr = indptr;
+    a.kv_indices = indices;
+    a.kv_last = last;
+    a.out = static_cast<_Float16*>(out);
+    a.lse = lse;
+    a.desc_b0 = reinterpret_cast<const int32_t*>(base + pl->off_desc);
+    a.empty_seq = reinterpret_cast<const int32_t*>(base + pl->off_empty);
+    a.counters = reinterpret_cast<int32_t*>(base + pl->off_cnt);
+    a.part_lse = reinterpret_cast<float*>(base + pl->off_plse);
+    a.part_o = reinterpret_cast<float*>(base + pl->off_po);
+    a.extra_o = extra_o;
+    a.extra_lse = extra_lse;
+    a.n_extra = n_extra;
+    a.extra_stride = n_extra;
+    a.U = pl->U;
+    a.nnz = pl->nnz;
+    a.jbase = pl->jbase;
+    a.B = pl->B;
+    a.Hq = pl->Hq;
+    a.Hkv = pl->Hkv;
+    a.W = pl->W;
+    a.n_empty = pl->n_empty;
+    a.b_first = pl->b_first;
+    a.scale_log2 = sm_scale * 1.4426950408889634f;
+    PD_HIP(launch_decode_streamk(a, pl->G, s));
+    return PDATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* pdattn_strerror(int status) {
+    switch (status) {
+        case PDATTN_OK: return "PDATTN_OK";
+        case PDATTN_ERR_INVALID_ARGUMENT: return "PDATTN_ERR_INVALID_ARGUMENT";
+        case PDATTN_ERR_UNSUPPORTED: return "PDATTN_ERR_UNSUPPORTED";
+        case PDATTN_ERR_PAGE_TABLE: return "PDATTN_ERR_PAGE_TABLE";
+        case PDATTN_ERR_WORKSPACE: return "PDATTN_ERR_WORKSPACE";
+        case PDATTN_ERR_HIP: return "PDATTN_ERR_HIP";
+        case PDATTN_ERR_NOT_READY: return "PDATTN_ERR_NOT_READY";
+        default: return "PDATTN_ERR_UNKNOWN";
+    }
+}
+
+const char* pdattn_last_error(void) { return g_last_error.c_str(); }
+
+int pdattn_workspace_reserve(pdattn_workspace* ws, size_t bytes) {
+    if (!ws) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null workspace");
+    if (ws->base && ws->bytes >= bytes) return PDATTN_OK;
+    if (ws->base && !ws->owned)
+        return fail(PDATTN_ERR_WORKSPACE, "caller-provided workspace holds %zu bytes, %zu needed", ws->bytes, bytes);
+    if (ws->base) {
+        PD_HIP(hipDeviceSynchronize());
+        PD_HIP(hipFree(ws->base));
+        ws->base = nullptr;
+        ws->bytes = 0;
+    }
+    void* p = nullptr;
+    PD_HIP(hipMalloc(&p, std::max<size_t>(bytes, kAlign)));
+    ws->base = p;
+    ws->bytes = std::max<size_t>(bytes, kAlign);
+    ws->owned = 1;
+    return PDATTN_OK;
+}
+
+void pdattn_workspace_release(pdattn_workspace* ws) {
+    if (!ws) return;
+    if (ws->base && ws->owned) {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(ws->base);
+    }
+    ws->base = nullptr;
+    ws->bytes = 0;
+    ws->owned = 0;
+}
+
+int pdattn_plan_chunks(int G, int variant, int B, int Hkv, int max_len, int force_chunks,
+                       int* num_chunks, int* chunk_tokens) {
+    if (!num_chunks || !chunk_tokens) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null output");
+    if (!valid_group(G)) return fail(PDATTN_ERR_UNSUPPORTED, "GQA group size %d not in {1,2,4,8}", G);
+    if (variant < 0 || variant > 3) return fail(PDATTN_ERR_INVALID_ARGUMENT, "variant %d not in 0..3", variant);
+    if (B < 0 || Hkv <= 0 || max_len < 0 || force_chunks < 0)
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "B=%d Hkv=%d max_len=%d force=%d", B, Hkv, max_len, force_chunks);
+    int chunks;
+    if (force_chunks > 0) {
+        chunks = force_chunks;
+    } else {
+        DeviceFacts f;
+        if (int st = device_facts(&f)) return st;
+        // one full wave of resident workgroups, rounded down; chunks of at least 256 tokens
+        const int64_t resident = (int64_t)f.cus * std::max(1, f.occ_partial[G]);
+        const int64_t want = std::max<int64_t>(1, resident / std::max<int64_t>(1, (int64_t)B * Hkv));
+        const int64_t cap = std::max<int64_t>(1, ((int64_t)max_len + 255) / 256);
+        chunks = (int)std::min(want, cap);
+    }
+    const int per = (max_len + chunks - 1) / chunks;
+    int tokens = (per + kPage - 1) / kPage * kPage;  // whole pages per chunk
+    if (tokens < kPage) tokens = kPage;
+    *chunk_tokens = tokens;
+    *num_chunks = std::max(1, (max_len + tokens - 1) / tokens);
+    return PDATTN_OK;
+}
+
+int pdattn_decode_partial(const pdattn_decode_params* p, int G, int variant, void* stream) {
+    if (variant < 0 || variant > 3) return fail(PDATTN_ERR_INVALID_ARGUMENT, "variant %d not in 0..3", variant);
+    if (int st = check_decode_params(p, G)) return st;
+    if (p->B == 0) return PDATTN_OK;
+    if (!p->part_o || !p->part_lse) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null part_o / part_lse");
+    PD_HIP(launch_decode_partial(to_partial_args(p), G, static_cast<hipStream_t>(stream)));
+    return PDATTN_OK;
+}
+
+int pdattn_merge_states(const float* part_o, const float* part_lse, void* out, float* lse_out,
+                        int rows, int num_chunks, void* stream) {
+    if (rows < 0 || num_chunks < 1) return fail(PDATTN_ERR_INVALID_ARGUMENT, "rows=%d num_chunks=%d", rows, num_chunks);
+    if (rows == 0) return PDATTN_OK;
+    if (!part_o || !part_lse || !out || !lse_out) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null pointer");
+    PD_HIP(launch_merge_states(part_o, part_lse, static_cast<_Float16*>(out), lse_out, rows, num_chunks,
+                               static_cast<hipStream_t>(stream)));
+    return PDATTN_OK;
+}
+
+size_t pdattn_decode_workspace_size(int B, int Hq, int part_stride) {
+    if (B < 0 || Hq < 0 || part_stride < 0) return 0;
+    const size_t rows = (size_t)B * Hq * part_stride;
+    return align_up(rows * kHeadDim * sizeof(float)) + align_up(rows * sizeof(float));
+}
+
+int pdattn_workspace_partials(const pdattn_workspace* ws, int B, int Hq, int part_stride,
+                              float** part_o, float** part_lse) {
+    if (!ws || !part_o || !part_lse) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null pointer");
+    const size_t need = pdattn_decode_workspace_size(B, Hq, part_stride);
+    if (!ws->base || ws->bytes < need) return fail(PDATTN_ERR_WORKSPACE, "workspace smaller than %zu bytes", need);
+    const size_t rows = (size_t)B * Hq * part_stride;
+    *part_o = static_cast<float*>(ws->base);
+    *part_lse = reinterpret_cast<float*>(static_cast<char*>(ws->base) + align_up(rows * kHeadDim * sizeof(float)));
+    return PDATTN_OK;
+}
+
+int pdattn_decode_attention(const pdattn_decode_params* p, int G, int variant, void* out,
+                            float* lse, pdattn_workspace* ws, void* stream) {
+    if (variant < 0 || variant > 3) return fail(PDATTN_ERR_INVALID_ARGUMENT, "variant %d not in 0..3", variant);
+    if (int st = check_decode_params(p, G)) return st;
+    if (p->B == 0) return PDATTN_OK;
+    if (!out || !lse) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null out / lse");
+    // the merge reads part_stride slots per row: every one of them must be written by this call
+    if (p->chunk_base != 0 || p->part_stride != p->num_chunks)
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "decode_attention needs chunk_base = 0 and part_stride = num_chunks");
+    const size_t need = pdattn_decode_workspace_size(p->B, p->Hq, p->part_stride);
+    if (int st = ensure_ws(ws, need)) return st;
+    pdattn_decode_params q = *p;
+    if (int st = pdattn_workspace_partials(ws, p->B, p->Hq, p->part_stride, &q.part_o, &q.part_lse)) return st;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    PD_HIP(launch_decode_partial(to_partial_args(&q), G, s));
+    PD_HIP(launch_merge_states(q.part_o, q.part_lse, static_cast<_Float16*>(out), lse, p->B * p->Hq,
+                               p->part_stride, s));
+    return PDATTN_OK;
+}
+
+int pdattn_plan_create(const int32_t* h_kv_indptr, const int32_t* h_kv_last_page_len, int B,
+                       int Hq, int Hkv, int force_workgroups, pdattn_plan** plan) {
+    if (!plan) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null plan output");
+    *plan = nullptr;
+    if (B > 0 && !h_kv_indptr) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null kv_indptr");
+    pdattn_plan* pl = new pdattn_plan();
+    if (int st = build_streamk_plan(h_kv_indptr, h_kv_last_page_len, B, Hq, Hkv, force_workgroups, pl)) {
+        free_plan_storage(pl);
+        delete pl;
+        return st;
+    }
+    *plan = pl;
+    return PDATTN_OK;
+}
+
+int pdattn_plan_get_info(const pdattn_plan* pl, pdattn_plan_info* info) {
+    if (!pl || !info) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null pointer");
+    info->workgroups = pl->W;
+    info->pairs = pl->B * pl->Hkv;
+    info->split_pairs = pl->split_pairs;
+    info->max_contributors = pl->max_contrib;
+    info->units = pl->U;
+    info->workspace_bytes = pl->ws_bytes;
+    return PDATTN_OK;
+}
+
+size_t pdattn_plan_workspace_size(const pdattn_plan* pl) { return pl ? pl->ws_bytes : 0; }
+
+int pdattn_plan_upload(pdattn_plan* pl, void* workspace, size_t bytes, void* stream) {
+    if (!pl) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null plan");
+    return upload_streamk(pl, workspace, bytes, static_cast<hipStream_t>(stream));
+}
+
+int pdattn_plan_run(const pdattn_plan* pl, const void* q, const void* k_cache, const void* v_cache,
+                    const int32_t* kv_indptr, const int32_t* kv_indices,
+                    const int32_t* kv_last_page_len, float sm_scale, void* out, float* lse,
+                    void* workspace, size_t bytes, void* stream) {
+    if (!pl) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null plan");
+    return run_streamk(pl, q, k_cache, v_cache, kv_indptr, kv_indices, kv_last_page_len, sm_scale,
+                       out, lse, workspace, bytes, static_cast<hipStream_t>(stream));
+}
+
+void pdattn_plan_destroy(pdattn_plan* pl) {
+    if (!pl) return;
+    free_plan_storage(pl);
+    delete pl;
+}
+
+int pdattn_shared_prefix_pages(const int32_t* h_indptr, const int32_t* h_indices, int B) {
+    if (B < 0 || !h_indptr || (B > 0 && !h_indices)) return -fail(PDATTN_ERR_INVALID_ARGUMENT, "null table or B < 0");
+    for (int b = 0; b < B; ++b)
+        if (h_indptr[b + 1] < h_indptr[b]) return -fail(PDATTN_ERR_PAGE_TABLE, "indptr not monotone at %d", b);
+    if (B < 2) return 0;
+    // longest P with indices[indptr[b] + i] equal across b for i < P, P <= npages_b - 1 for all b
+    for (int P = 0;; ++P) {
+        for (int b = 0; b < B; ++b)
+            if (P >= h_indptr[b + 1] - h_indptr[b] - 1) return P;
+        const int pg = h_indices[h_indptr[0] + P];
+        for (int b = 1; b < B; ++b)
+            if (h_indices[h_indptr[b] + P] != pg) return P;
+    }
+}
+
+int pdattn_cascade_prefix(const pdattn_prefix_params* p, void* stream) {
+    if (!p) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null params");
+    int G = 0;
+    if (int st = check_heads(p->Hq, p->Hkv, &G)) return st;
+    if (p->B < 0 || p->prefix_len < 0) return fail(PDATTN_ERR_INVALID_ARGUMENT, "B / prefix_len negative");
+    if (p->B == 0 || p->prefix_len == 0) return PDATTN_OK;
+    if (!p->q || !p->k_cache || !p->v_cache || !p->prefix_pages || !p->part_o || !p->part_lse)
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "null device pointer");
+    if (!aligned16(p->q) || !aligned16(p->k_cache) || !aligned16(p->v_cache) || !aligned16(p->part_o))
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "q / caches / part_o must be 16-byte aligned");
+    if (p->chunk_tokens < kPage || p->chunk_tokens % kPage || p->chunk_tokens > 8192)
+        return fail(PDATTN_ERR_UNSUPPORTED, "chunk_tokens=%d must be a multiple of 16 in [16, 8192]", p->chunk_tokens);
+    const int nchunks = (p->prefix_len + p->chunk_tokens - 1) / p->chunk_tokens;
+    if (p->part_stride < nchunks)
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "part_stride=%d < %d prefix chunks", p->part_stride, nchunks);
+    PrefixArgs a;
+    a.q = static_cast<const _Float16*>(p->q);
+    a.k = static_cast<const uint8_t*>(p->k_cache);
+    a.v = static_cast<const uint8_t*>(p->v_cache);
+    a.prefix_pages = p->prefix_pages;
+    a.part_o = p->part_o;
+    a.part_lse = p->part_lse;
+    a.B = p->B;
+    a.Hq = p->Hq;
+    a.Hkv = p->Hkv;
+    a.prefix_len = p->prefix_len;
+    a.chunk_tokens = p->chunk_tokens;
+    a.part_stride = p->part_stride;
+    a.num_chunks = nchunks;
+    a.scale_log2 = p->sm_scale * 1.4426950408889634f;
+    const int rows = prefix_rows_per_workgroup();
+    const int qtiles = (p->B * G + rows - 1) / rows;
+    PD_HIP(launch_cascade_prefix(a, G, qtiles, static_cast<hipStream_t>(stream)));
+    return PDATTN_OK;
+}
+
+int pdattn_cascade_plan_create(const pdattn_decode_params* base, const int32_t* h_indptr,
+                               const int32_t* h_indices, const int32_t* h_lens,
+                               const int32_t* d_indices, int min_prefix,
+                               pdattn_cascade_plan** plan) {
+    if (!plan) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null plan output");
+    *plan = nullptr;
+    if (!base) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null base params");
+    int G = 0;
+    if (int st = check_heads(base->Hq, base->Hkv, &G)) return st;
+    const int B = base->B;
+    if (B < 0) return fail(PDATTN_ERR_INVALID_ARGUMENT, "B=%d is negative", B);
+    if (base->kv_start != 0) return fail(PDATTN_ERR_INVALID_ARGUMENT, "cascade base must have kv_start = 0");
+    if (B > 0 && (!h_indptr || !h_indices || !h_lens || !d_indices))
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "null host table / lens / device indices");
+    if (B > 0 && (!base->q || !base->k_cache || !base->v_cache || !base->kv_indptr || !base->kv_indices ||
+                  !base->kv_last_page_len))
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "null device pointer in base params");
+    if (!std::isfinite(base->sm_scale)) return fail(PDATTN_ERR_INVALID_ARGUMENT, "sm_scale is not finite");
+    // last-page lengths from the sequence lengths (ceil(L/16) pages each)
+    std::vector<int32_t> last(std::max(1, B), 0);
+    for (int b = 0; b < B; ++b) {
+        const int np = h_indptr[b + 1] - h_indptr[b];
+        if (np < 0) return fail(PDATTN_ERR_PAGE_TABLE, "indptr not monotone at %d", b);
+        if (h_lens[b] < 0 || (h_lens[b] + kPage - 1) / kPage != np)
+            return fail(PDATTN_ERR_PAGE_TABLE, "lens[%d]=%d does not match its %d pages", b, h_lens[b], np);
+        last[b] = np > 0 ? h_lens[b] - (np - 1) * kPage : 0;
+    }
+    DeviceFacts f;
+    if (int st = device_facts(&f)) return st;
+
+    pdattn_cascade_plan* cp = new pdattn_cascade_plan();
+    cp->base = *base;
+    const int P = B > 0 ? pdattn_shared_prefix_pages(h_indptr, h_indices, B) : 0;
+    if (P < 0) { delete cp; return -P; }
+    cp->P = P;
+    cp->Lp = P * kPage;
+    cp->use = (cp->Lp > 0 && cp->Lp >= min_prefix) ? 1 : 0;
+    int st = PDATTN_OK;
+    if (!cp->use) {
+        st = build_streamk_plan(h_indptr, last.data(), B, base->Hq, base->Hkv, 0, &cp->sk);
+        cp->off_sk = 0;
+        cp->ws_bytes = cp->sk.ws_bytes;
+    } else {
+        // prefix chunks: about one wave of prefix workgroups, chunks of >= 256 keys, <= 8192
+        cp->qgroups = (B * G + prefix_rows_per_workgroup() - 1) / prefix_rows_per_workgroup();
+        const int target = f.cus * std::max(1, f.occ_prefix[G]);
+        int cpre = std::max(1, target / (cp->qgroups * base->Hkv));
+        cpre = std::min(cpre, std::max(1, cp->Lp / 256));
+        int ctok = ((cp->Lp + cpre - 1) / cpre + 63) / 64 * 64;
+        ctok = std::min(ctok, 8192);
+        cp->ctok = ctok;
+        cp->cpre = (cp->Lp + ctok - 1) / ctok;
+        cp->d_prefix_pages = d_indices + h_indptr[0];
+        // compacted suffix page table: pages P.. of every sequence
+        std::vector<int32_t> sind(B + 1, 0);
+        std::vector<int32_t> sidx;
+        for (int b = 0; b < B; ++b) {
+            for (int i = h_indptr[b] + P; i < h_indptr[b + 1]; ++i) sidx.push_back(h_indices[i]);
+            sind[b + 1] = (int32_t)sidx.size();
+        }
+        st = build_streamk_plan(sind.data(), last.data(), B, base->Hq, base->Hkv, 0, &cp->sk);
+        cp->tbl = sind;
+        cp->tbl.insert(cp->tbl.end(), sidx.begin(), sidx.end());
+        const size_t rows = (size_t)B * base->Hq;
+        size_t off = 0;
+        cp->off_ppo = off;   off += align_up(rows * cp->cpre * kHeadDim * sizeof(float));
+        cp->off_pplse = off; off += align_up(rows * cp->cpre * sizeof(float));
+        cp->off_tbl = off;   off += align_up(cp->tbl.size() * sizeof(int32_t));
+        cp->off_sk = off;    off += cp->sk.ws_bytes;
+        cp->ws_bytes = off;
+    }
+    if (st != PDATTN_OK) {
+        pdattn_cascade_plan_destroy(cp);
+        return st;
+    }
+    *plan = cp;
+    return PDATTN_OK;
+}
+
+int pdattn_cascade_plan_get_info(const pdattn_cascade_plan* cp, pdattn_cascade_info* info) {
+    if (!cp || !info) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null pointer");
+    info->use = cp->use;
+    info->prefix_tokens = cp->Lp;
+    info->prefix_chunks = cp->cpre;
+    info->prefix_workgroups = cp->use ? cp->cpre * cp->qgroups * cp->base.Hkv : 0;
+    info->suffix_workgroups = cp->sk.W;
+    info->workspace_bytes = cp->ws_bytes;
+    return PDATTN_OK;
+}
+
+int pdattn_cascade_decode(pdattn_cascade_plan* cp, void* out, float* lse, pdattn_workspace* ws,
+                          void* stream) {
+    if (!cp) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null plan");
+    if (cp->base.B == 0) return PDATTN_OK;
+    if (!out || !lse) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null out / lse");
+    if (int st = ensure_ws(ws, cp->ws_bytes)) return st;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    char* base = static_cast<char*>(ws->base);
+    const pdattn_decode_params& p = cp->base;
+    if (cp->uploaded_to != ws->base) {
+        if (cp->use && !cp->pinned) {
+            hipError_t e = hipHostMalloc(&cp->pinned, cp->tbl.size() * sizeof(int32_t), hipHostMallocDefault);
+            if (e != hipSuccess) return hip_fail(e, "hipHostMalloc(cascade plan)");
+            std::memcpy(cp->pinned, cp->tbl.data(), cp->tbl.size() * sizeof(int32_t));
+        }
+        if (cp->use)
+            PD_HIP(hipMemcpyAsync(base + cp->off_tbl, cp->pinned, cp->tbl.size() * sizeof(int32_t),
+                                  hipMemcpyHostToDevice, s));
+        if (int st = upload_streamk(&cp->sk, base + cp->off_sk, cp->sk.ws_bytes, s)) return st;
+        cp->uploaded_to = ws->base;
+    }
+    if (!cp->use)
+        return run_streamk(&cp->sk, p.q, p.k_cache, p.v_cache, p.kv_indptr, p.kv_indices,
+                           p.kv_last_page_len, p.sm_scale, out, lse, base + cp->off_sk, cp->sk.ws_bytes, s);
+    float* ppo = reinterpret_cast<float*>(base + cp->off_ppo);
+    float* pplse = reinterpret_cast<float*>(base + cp->off_pplse);
+    pdattn_prefix_params pp;
+    pp.q = p.q;
+    pp.k_cache = p.k_cache;
+    pp.v_cache = p.v_cache;
+    pp.prefix_pages = cp->d_prefix_pages;
+    pp.part_o = ppo;
+    pp.part_lse = pplse;
+    pp.B = p.B;
+    pp.Hq = p.Hq;
+    pp.Hkv = p.Hkv;
+    pp.prefix_len = cp->Lp;
+    pp.chunk_tokens = cp->ctok;
+    pp.part_stride = cp->cpre;
+    pp.sm_scale = p.sm_scale;
+    if (int st = pdattn_cascade_prefix(&pp, stream)) return st;
+    const int32_t* sind = reinterpret_cast<const int32_t*>(base + cp->off_tbl);
+    const int32_t* sidx = sind + (p.B + 1);
+    return run_streamk(&cp->sk, p.q, p.k_cache, p.v_cache, sind, sidx, p.kv_last_page_len, p.sm_scale,
+                       out, lse, base + cp->off_sk, cp->sk.ws_bytes, s, ppo, pplse, cp->cpre);
+}
+
+void pdattn_cascade_plan_destroy(pdattn_cascade_plan* cp) {
+    if (!cp) return;
+    free_plan_storage(&cp->sk);
+    if (cp->pinned) (void)hipHostFree(cp->pinned);
+    delete cp;
+}
+
+int pdattn_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream) {
+    if (!buf || !sink || bytes % 16) return fail(PDATTN_ERR_INVALID_ARGUMENT, "buf/sink null or bytes %% 16 != 0");
+    if (bytes == 0) return PDATTN_OK;
+    DeviceFacts f;
+    if (int st = device_facts(&f)) return st;
+    PD_HIP(launch_stream_read(buf, bytes, sink, f.cus * 16, static_cast<hipStream_t>(stream)));
+    return PDATTN_OK;
+}
+
+int pdattn_flush_cache(void* buf, size_t bytes, void* stream) {
+    if (!buf || bytes % 16) return fail(PDATTN_ERR_INVALID_ARGUMENT, "buf null or bytes %% 16 != 0");
+    if (bytes == 0) return PDATTN_OK;
+    DeviceFacts f;
+    if (int st = device_facts(&f)) return st;
+    PD_HIP(launch_flush(buf, bytes, f.cus * 16, static_cast<hipStream_t>(stream)));
+    return PDATTN_OK;
+}
+
+int pdattn_get_device_info(pdattn_device_info* info) {
+    if (!info) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null info");
+    DeviceFacts f;
+    if (int st = device_facts(&f)) return st;
+    info->compute_units = f.cus;
+    info->decode_wg_per_cu = f.occ_streamk[4];
+    info->prefix_wg_per_cu = f.occ_prefix[4];
+    snprintf(info->arch, sizeof info->arch, "%s", f.arch);
+    return PDATTN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,278 @@
+// cascade.hip -- shared-prefix ("cascade") attention on CDNA4 fp16 MFMA.
+//
+// With prefix caching, all B sequences of a batch start with the same physical pages. Their
+// B*G query rows per kv head (G = Hq/Hkv) are stacked into one matrix and attend to the shared
+// keys once, as a dense contraction (qilem/cuda-kernel-lab, 01_decode_attention.cu:446-632 does
+// the same with WMMA in two passes). Here it is a single pass with an online softmax:
+//
+//   S^T = K Q^T   (v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims, B = 32 dims x 16 queries)
+//   O^T += V^T P^T (A = 16 dims x 32 keys, B = 32 keys x 16 queries)
+//
+// Computing the transposed products puts one query per lane column of every 16x16 accumulator
+// (lane l holds rows 4*(l/16)+j, column l%16), so
+//   * the running max / sum of a query live in the lanes of that column: a row max over a key
+//     tile is an in-lane max plus two cross-lane steps, and the rescale of the output
+//     accumulator by exp(m_old - m_new) is a per-lane scalar multiply;
+//   * P leaves the S^T accumulator already in the B-operand layout of the PV product (the 8
+//     keys a lane contributes are 4 of one 16-key tile and 4 of the next; V^T is read with the
+//     same key order), so P needs no cross-lane movement.
+// K is staged in LDS as [key][16-byte chunk] with the chunk index XOR-ed by (key & 15): the
+// A-operand reads (16 keys x one chunk per 16-lane phase) hit 16 distinct bank groups. V is
+// staged transposed (V^T[dim][key pair], rows padded to 33 dwords) so that the A operand of the
+// PV product is two conflict-free 8-byte reads. Two LDS buffers: the global loads of block n+1
+// are in flight while block n is computed.
+//
+// A workgroup: 4 waves x 4 query tiles x 16 = 256 stacked query rows of one kv head, one
+// chunk of prefix keys, written as the normalized partial (o, lse) of that chunk.
+#include <math.h>
+
+#include "pdattn_internal.h"
+
+namespace pdattn {
+namespace {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLn2 = 0.69314718055994531f;
+constexpr int PW = 4;               // waves per workgroup
+constexpr int PT = PW * 64;         // threads per workgroup
+constexpr int QT = 4;               // 16-query tiles per wave
+constexpr int QROWS = PW * QT * 16; // stacked query rows per workgroup
+constexpr int KB = 64;              // keys per LDS block
+constexpr int VTS = 33;             // V^T row stride in dwords (32 key pairs + 1 pad)
+constexpr int MAXPG = 512;          // pages per chunk, i.e. chunk_tokens <= 8192
+
+struct PSmem {
+    u32x4 K[2][KB][16];              // [key][chunk ^ (key & 15)], 16 bytes = 8 dims per chunk
+    uint32_t VT[2][kHeadDim][VTS];   // [dim][key pair]: low half key 2p, high half key 2p+1
+    int pg[MAXPG];                   // physical pages of this chunk
+};
+
+__device__ __forceinline__ f32x4 mfma16x16x32(const f16x8& a, const f16x8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
+    __shared__ PSmem sm;
+    const int chunk = blockIdx.x, qgrp = blockIdx.y, kvh = blockIdx.z;
+    const int G = a.Hq / a.Hkv, nq = a.B * G;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int kbeg = chunk * a.chunk_tokens;
+    const int kend = min(a.prefix_len, kbeg + a.chunk_tokens);
+    const int nkeys = max(0, kend - kbeg);
+    const int npg = (nkeys + kPage - 1) / kPage;
+    const int nblk = (nkeys + KB - 1) / KB;
+    const size_t page_bytes = (size_t)kPage * a.Hkv * 256;
+
+    for (int i = tid; i < npg; i += PT) sm.pg[i] = a.prefix_pages[kbeg / kPage + i];
+
+    // B operands of S^T: Q[query][32 ks + 8 lg .. +7], query = l16 of tile tq
+    f16x8 qb[QT][4];
+    int qrow[QT];
+#pragma unroll
+    for (int tq = 0; tq < QT; ++tq) {
+        const int qi = qgrp * QROWS + (wave * QT + tq) * 16 + l16;
+        qrow[tq] = -1;
+        if (qi < nq) {
+            const int b = qi / G, g = qi % G;
+            qrow[tq] = b * a.Hq + kvh * G + g;
+            const _Float16* qp = a.q + (size_t)qrow[tq] * kHeadDim + 8 * lg;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) qb[tq][ks] = *reinterpret_cast<const f16x8*>(qp + 32 * ks);
+        } else {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) qb[tq][ks] = f16x8{};
+        }
+    }
+
+    f32x4 acc[QT][8];
+    float m_run[QT], l_run[QT];
+#pragma unroll
+    for (int tq = 0; tq < QT; ++tq) {
+        m_run[tq] = -INFINITY;
+        l_run[tq] = 0.f;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) acc[tq][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // staging: K rows tid/16 + 16 i, chunk tid%16; V rows 2 kp (+1) + 32 s, kp = tid/16
+    const int sc = tid & 15, sr = tid >> 4;
+    u32x4 kst[4], vst[4];
+    auto gload = [&](int kb) {
+        const int key0 = kbeg + kb * KB;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = key0 + sr + 16 * i;
+            kst[i] = u32x4{0u, 0u, 0u, 0u};
+            if (key < kend) {
+                const size_t pid = (uint32_t)sm.pg[(key - kbeg) >> 4];
+                kst[i] = *reinterpret_cast<const u32x4*>(a.k + pid * page_bytes +
+                                                         (size_t)(((key & 15) * a.Hkv + kvh) * 256 + sc * 16));
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = key0 + 2 * sr + (i & 1) + 32 * (i >> 1);
+            vst[i] = u32x4{0u, 0u, 0u, 0u};
+            if (key < kend) {
+                const size_t pid = (uint32_t)sm.pg[(key - kbeg) >> 4];
+                vst[i] = *reinterpret_cast<const u32x4*>(a.v + pid * page_bytes +
+                                                         (size_t)(((key & 15) * a.Hkv + kvh) * 256 + sc * 16));
+            }
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int n = sr + 16 * i;
+            sm.K[buf][n][sc ^ (n & 15)] = kst[i];
+        }
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const u32x4 lo = vst[2 * s], hi = vst[2 * s + 1];  // keys 2p and 2p+1, dims 8 sc .. +7
+            const int p = sr + 16 * s;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sm.VT[buf][8 * sc + 2 * e][p] = __builtin_amdgcn_perm(hi[e], lo[e], 0x05040100u);
+                sm.VT[buf][8 * sc + 2 * e + 1][p] = __builtin_amdgcn_perm(hi[e], lo[e], 0x07060302u);
+            }
+        }
+    };
+
+    __syncthreads();  // page ids
+    if (nblk > 0) {
+        gload(0);
+        lstore(0);
+    }
+    __syncthreads();
+
+    for (int kb = 0; kb < nblk; ++kb) {
+        const int buf = kb & 1;
+        const bool more = kb + 1 < nblk;
+        if (more) gload(kb + 1);
+
+        // S^T tiles: s[tq][tk][j] = score(key 16 tk + 4 lg + j, query l16 of tile tq)
+        f32x4 s[QT][4];
+#pragma unroll
+        for (int tk = 0; tk < 4; ++tk) {
+            f16x8 ka[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                ka[ks] = __builtin_bit_cast(f16x8, sm.K[buf][16 * tk + l16][(4 * ks + lg) ^ l16]);
+#pragma unroll
+            for (int tq = 0; tq < QT; ++tq) {
+                f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) c = mfma16x16x32(ka[ks], qb[tq][ks], c);
+                s[tq][tk] = c;
+            }
+        }
+
+        // online softmax (base 2) per query
+        const int kbase = kbeg + kb * KB + 4 * lg;
+        float mn[QT];
+        bool grow = false;
+#pragma unroll
+        for (int tq = 0; tq < QT; ++tq) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int tk = 0; tk < 4; ++tk)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const bool ok = kbase + 16 * tk + j < kend;
+                    const float x = ok ? s[tq][tk][j] * a.scale_log2 : -INFINITY;
+                    s[tq][tk][j] = x;
+                    mx = fmaxf(mx, x);
+                }
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            mn[tq] = fmaxf(m_run[tq], mx);
+            grow |= mn[tq] > m_run[tq];
+        }
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+            for (int tq = 0; tq < QT; ++tq) {
+                const float al = (mn[tq] > m_run[tq]) ? __builtin_amdgcn_exp2f(m_run[tq] - mn[tq]) : 1.f;
+                l_run[tq] *= al;
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt) acc[tq][dt] *= al;
+                m_run[tq] = mn[tq];
+            }
+        }
+        f16x8 pb[QT][2];
+#pragma unroll
+        for (int tq = 0; tq < QT; ++tq) {
+            const float ms = (m_run[tq] == -INFINITY) ? 0.f : m_run[tq];
+#pragma unroll
+            for (int tk = 0; tk < 4; ++tk)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float p = __builtin_amdgcn_exp2f(s[tq][tk][j] - ms);
+                    l_run[tq] += p;   // fp32 weights for the denominator (exact lse); PV uses
+                    pb[tq][tk >> 1][(tk & 1) * 4 + j] = (_Float16)p;   // them rounded to nearest
+                }
+        }
+
+        // O^T += V^T P^T
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            const int d = 16 * dt + l16;
+#pragma unroll
+            for (int kb2 = 0; kb2 < 2; ++kb2) {
+                const int p0 = 16 * kb2 + 2 * lg;
+                u32x4 raw;
+                raw[0] = sm.VT[buf][d][p0];
+                raw[1] = sm.VT[buf][d][p0 + 1];
+                raw[2] = sm.VT[buf][d][p0 + 8];
+                raw[3] = sm.VT[buf][d][p0 + 9];
+                const f16x8 va = __builtin_bit_cast(f16x8, raw);
+#pragma unroll
+                for (int tq = 0; tq < QT; ++tq) acc[tq][dt] = mfma16x16x32(va, pb[tq][kb2], acc[tq][dt]);
+            }
+        }
+
+        if (more) lstore(buf ^ 1);
+        __syncthreads();
+    }
+
+    // normalized partial of this chunk
+#pragma unroll
+    for (int tq = 0; tq < QT; ++tq) {
+        float L = l_run[tq];
+        L += __shfl_xor(L, 16);
+        L += __shfl_xor(L, 32);
+        if (qrow[tq] < 0) continue;
+        const size_t slot = (size_t)qrow[tq] * a.part_stride + chunk;
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        float* po = a.part_o + slot * kHeadDim + 4 * lg;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(po + 16 * dt) = acc[tq][dt] * inv;
+        if (lg == 0)
+            a.part_lse[slot] = L > 0.f ? (m_run[tq] + __builtin_amdgcn_logf(L)) * kLn2 : -INFINITY;
+    }
+}
+
+}  // namespace
+
+int prefix_rows_per_workgroup() { return QROWS; }
+
+hipError_t launch_cascade_prefix(const PrefixArgs& a, int G, int qtiles, hipStream_t s) {
+    (void)G;
+    if (a.num_chunks <= 0 || qtiles <= 0 || a.Hkv <= 0) return hipSuccess;
+    dim3 grid(a.num_chunks, qtiles, a.Hkv);
+    cascade_prefix_kernel<<<grid, PT, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+int occupancy_cascade_prefix(int G) {
+    (void)G;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&cascade_prefix_kernel), PT, 0) != hipSuccess)
+        return 1;
+    return n > 0 ? n : 1;
+}
+
+}  // namespace pdattn

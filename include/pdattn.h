@@ -1,0 +1,230 @@
+/*
+ * pdattn.h -- C ABI of the MI355X (gfx950) paged split-KV GQA decode attention library.
+ *
+ * Drop-in boundary for the decode-attention path of qilem/cuda-kernel-lab
+ * (01_decode_attention.cu). That file has no extern "C" layer: its interface is a set of C++
+ * free functions and kernels called from its own main(). Each entry point below replaces one of
+ * them (cited at the declaration) with the same argument meaning, exposed as plain C so that any
+ * FFI (ctypes, cgo, JNI, N-API) can bind it:
+ *   - device pointers are passed as `void*` / typed pointers, sizes as ints / size_t;
+ *   - a HIP stream is passed as `void*` (a hipStream_t; NULL = the default stream);
+ *   - every function returns a pdattn_status (0 = success) instead of calling exit(), which is
+ *     what the reference does on any error (common/bench.cuh:21-29, 01:285-286).
+ *
+ * Tensor layouts (identical to the reference, 01_decode_attention.cu:5-9, 112):
+ *   q          [B, Hq, 128]                fp16
+ *   k_cache,
+ *   v_cache    [num_pages, 16, Hkv, 128]   fp16; element (page, slot, kvh, d) at
+ *                                          ((page*16 + slot)*Hkv + kvh)*128 + d
+ *   kv_indptr [B+1], kv_indices [nnz], kv_last_page_len [B]   int32 CSR page table (FlashInfer)
+ *   out        [B, Hq, 128] fp16;  lse [B, Hq] fp32 (natural log of the scaled scores)
+ * q head h reads kv head h / G with G = Hq / Hkv in {1, 2, 4, 8}; head_dim is 128; page size 16.
+ * An empty sequence (no pages) yields out = 0, lse = -inf.
+ */
+#ifndef PDATTN_H
+#define PDATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PDATTN_HEAD_DIM 128
+#define PDATTN_PAGE_SIZE 16
+
+typedef enum pdattn_status {
+    PDATTN_OK = 0,
+    PDATTN_ERR_INVALID_ARGUMENT = 1, /* null pointer, negative size, inconsistent chunking      */
+    PDATTN_ERR_UNSUPPORTED = 2,      /* G not in {1,2,4,8}, Hq % Hkv != 0                        */
+    PDATTN_ERR_PAGE_TABLE = 3,       /* indptr not monotone, last_page_len outside [1,16]        */
+    PDATTN_ERR_WORKSPACE = 4,        /* caller-provided workspace smaller than required          */
+    PDATTN_ERR_HIP = 5,              /* a HIP runtime call failed (detail in pdattn_last_error)  */
+    PDATTN_ERR_NOT_READY = 6         /* plan not uploaded into this workspace                    */
+} pdattn_status;
+
+/* Name of a status code. */
+const char* pdattn_strerror(int status);
+/* Detail message of the last failing call on this host thread ("" if none). */
+const char* pdattn_last_error(void);
+
+/* Launch argument block. Same fields, order and meaning as DecodeParams
+ * (01_decode_attention.cu:51-65). part_o is [B*Hq, part_stride, 128] fp32 holding normalized
+ * partial outputs; part_lse is [B*Hq, part_stride]. Chunk c of a sequence covers keys
+ * [kv_start + c*chunk_tokens, min(seq_len, kv_start + (c+1)*chunk_tokens)) and writes slot
+ * chunk_base + c. */
+typedef struct pdattn_decode_params {
+    const void*    q;
+    const void*    k_cache;
+    const void*    v_cache;
+    const int32_t* kv_indptr;
+    const int32_t* kv_indices;
+    const int32_t* kv_last_page_len;
+    float*         part_o;
+    float*         part_lse;
+    int32_t B, Hq, Hkv, num_chunks, chunk_tokens;
+    int32_t kv_start;
+    int32_t chunk_base;
+    int32_t part_stride;
+    float   sm_scale;
+} pdattn_decode_params;
+
+/* Device workspace. Replaces Workspace (01_decode_attention.cu:314). The reference grows its
+ * workspace inside decode_attention with cudaFree/cudaMalloc; here a workspace that the library
+ * allocated (owned = 1, or base == NULL) is grown the same way, while caller-provided memory
+ * (owned = 0) is never replaced: a call that needs more returns PDATTN_ERR_WORKSPACE. Reserve
+ * the required size up front (pdattn_workspace_reserve) to keep every call allocation-free. */
+typedef struct pdattn_workspace {
+    void*  base;
+    size_t bytes;
+    int    owned;
+} pdattn_workspace;
+
+/* Grow `ws` to at least `bytes` with hipMalloc (ensure_workspace, 01_decode_attention.cu:648-654).
+ * Synchronizes the device before freeing an old owned buffer. */
+int pdattn_workspace_reserve(pdattn_workspace* ws, size_t bytes);
+/* Free an owned workspace and zero the struct (the reference's cudaFree at 01:893). */
+void pdattn_workspace_release(pdattn_workspace* ws);
+
+/* ---- reference-shaped split-KV path (uniform chunks) ------------------------------------- */
+
+/* Chunk count for the uniform split (plan_chunks, 01_decode_attention.cu:289-312): about one full
+ * wave of resident workgroups over all CUs (hipOccupancyMaxActiveBlocksPerMultiprocessor x CU
+ * count, rounded down), chunks of at least 256 tokens, chunk_tokens a multiple of 16;
+ * force_chunks > 0 overrides. `variant` is accepted for signature parity and must be 0..3. */
+int pdattn_plan_chunks(int G, int variant, int B, int Hkv, int max_len, int force_chunks,
+                       int* num_chunks, int* chunk_tokens);
+
+/* Partial (o, lse) per chunk into p->part_o / p->part_lse; grid (num_chunks, B*Hkv)
+ * (decode_partial<G,V>, 01_decode_attention.cu:76-236, launched at 01:327-329). */
+int pdattn_decode_partial(const pdattn_decode_params* p, int G, int variant, void* stream);
+
+/* Log-sum-exp merge of `num_chunks` partial states for each of `rows` rows into fp16 out and
+ * fp32 lse; rows with every lse = -inf give 0 / -inf (merge_states, 01_decode_attention.cu:238-255). */
+int pdattn_merge_states(const float* part_o, const float* part_lse, void* out, float* lse_out,
+                        int rows, int num_chunks, void* stream);
+
+/* Bytes of workspace decode_attention needs for B*Hq rows of part_stride partial slots. */
+size_t pdattn_decode_workspace_size(int B, int Hq, int part_stride);
+
+/* Where decode_attention places part_o / part_lse inside a workspace (for reading per-chunk lse). */
+int pdattn_workspace_partials(const pdattn_workspace* ws, int B, int Hq, int part_stride,
+                              float** part_o, float** part_lse);
+
+/* Partial launch then merge launch on `stream`, partials in `ws`; p->part_o / p->part_lse are
+ * ignored and taken from the workspace (decode_attention, 01_decode_attention.cu:316-331). */
+int pdattn_decode_attention(const pdattn_decode_params* p, int G, int variant, void* out,
+                            float* lse, pdattn_workspace* ws, void* stream);
+
+/* ---- balanced single-launch path (stream-K plan / run) ----------------------------------- */
+/* The MI355X path for decode_attention: the planner (host, from the host copy of the page
+ * table, the way FlashInfer's plan() works) cuts the flattened (kv head, page) work of the whole
+ * batch into equal page ranges, one per workgroup of a single full wave over all CUs; ranges
+ * cross sequence boundaries freely. A workgroup writes the final out/lse of every sequence it
+ * covers completely; a sequence split over several workgroups is merged (fixed order, so the
+ * result is deterministic) by the last of them to finish, in the same launch. */
+typedef struct pdattn_plan pdattn_plan;
+
+typedef struct pdattn_plan_info {
+    int     workgroups;        /* grid size W                                             */
+    int     pairs;             /* B * Hkv                                                 */
+    int     split_pairs;       /* pairs covered by more than one workgroup                */
+    int     max_contributors;  /* most workgroups contributing to one pair                */
+    int64_t units;             /* Hkv * nnz pages                                         */
+    size_t  workspace_bytes;
+} pdattn_plan_info;
+
+/* Build a plan from host copies of kv_indptr [B+1] and kv_last_page_len [B]. force_workgroups > 0
+ * overrides the occupancy-derived grid size (it is clamped to the number of page units). */
+int pdattn_plan_create(const int32_t* h_kv_indptr, const int32_t* h_kv_last_page_len, int B,
+                       int Hq, int Hkv, int force_workgroups, pdattn_plan** plan);
+int pdattn_plan_get_info(const pdattn_plan* plan, pdattn_plan_info* info);
+size_t pdattn_plan_workspace_size(const pdattn_plan* plan);
+/* Stream-ordered copy of the plan's schedule into `workspace` and reset of its merge counters.
+ * Must precede pdattn_plan_run with that workspace; the plan may be run any number of times. */
+int pdattn_plan_upload(pdattn_plan* plan, void* workspace, size_t bytes, void* stream);
+/* One launch: attention for every (sequence, q head) of the planned batch. The device page table
+ * must hold the same values as the host copy the plan was built from. */
+int pdattn_plan_run(const pdattn_plan* plan, const void* q, const void* k_cache,
+                    const void* v_cache, const int32_t* kv_indptr, const int32_t* kv_indices,
+                    const int32_t* kv_last_page_len, float sm_scale, void* out, float* lse,
+                    void* workspace, size_t bytes, void* stream);
+void pdattn_plan_destroy(pdattn_plan* plan);
+
+/* ---- shared-prefix (cascade) path --------------------------------------------------------- */
+
+/* Longest run of physical pages that every sequence starts with, keeping at least one private
+ * page per sequence; 0 when B < 2 (shared_prefix_pages, 01_decode_attention.cu:634-646).
+ * Host arrays. Returns the page count (>= 0) or a negative pdattn_status. */
+int pdattn_shared_prefix_pages(const int32_t* h_indptr, const int32_t* h_indices, int B);
+
+/* Argument block of the prefix kernel. Same fields and meaning as PrefixParams
+ * (01_decode_attention.cu:473-482): prefix_pages are the physical pages of the shared prefix in
+ * order; the kernel writes partial slot `chunk` of every (sequence, q head) row it covers. */
+typedef struct pdattn_prefix_params {
+    const void*    q;
+    const void*    k_cache;
+    const void*    v_cache;
+    const int32_t* prefix_pages;
+    float*         part_o;
+    float*         part_lse;
+    int32_t B, Hq, Hkv, prefix_len, chunk_tokens, part_stride;
+    float   sm_scale;
+} pdattn_prefix_params;
+
+/* Prefix partials on fp16 MFMA, one partial slot per prefix chunk: slot c covers prefix keys
+ * [c*chunk_tokens, min(prefix_len, (c+1)*chunk_tokens)) (cascade_prefix,
+ * 01_decode_attention.cu:484-632; chunk count = ceil(prefix_len / chunk_tokens)). */
+int pdattn_cascade_prefix(const pdattn_prefix_params* p, void* stream);
+
+typedef struct pdattn_cascade_plan pdattn_cascade_plan;
+
+typedef struct pdattn_cascade_info {
+    int    use;             /* 1 when a shared prefix of >= min_prefix tokens was found  */
+    int    prefix_tokens;   /* Lp                                                       */
+    int    prefix_chunks;   /* prefix partial slots per row                            */
+    int    prefix_workgroups;
+    int    suffix_workgroups;
+    size_t workspace_bytes;
+} pdattn_cascade_info;
+
+/* Build the cascade plan (plan_cascade, 01_decode_attention.cu:664-701) from the launch block
+ * `base` (its q / caches / device page table / B / Hq / Hkv / sm_scale are used), host copies of
+ * indptr, indices and sequence lengths, the device kv_indices pointer, and min_prefix tokens
+ * (the reference's default is 256). When no prefix of at least min_prefix tokens is shared,
+ * info.use = 0 and pdattn_cascade_decode runs the plain balanced decode. */
+int pdattn_cascade_plan_create(const pdattn_decode_params* base, const int32_t* h_indptr,
+                               const int32_t* h_indices, const int32_t* h_lens,
+                               const int32_t* d_indices, int min_prefix,
+                               pdattn_cascade_plan** plan);
+int pdattn_cascade_plan_get_info(const pdattn_cascade_plan* plan, pdattn_cascade_info* info);
+/* Prefix kernel, suffix decode and merge on `stream` (cascade_decode, 01_decode_attention.cu:703-712).
+ * The first call with a given workspace uploads the plan's schedule into it (stream-ordered). */
+int pdattn_cascade_decode(pdattn_cascade_plan* plan, void* out, float* lse, pdattn_workspace* ws,
+                          void* stream);
+void pdattn_cascade_plan_destroy(pdattn_cascade_plan* plan);
+
+/* ---- measurement helpers ------------------------------------------------------------------ */
+
+/* Streams `bytes` (a multiple of 16) with 16-byte loads and folds them into one word, written
+ * to *sink only on a sentinel match (stream_read, 01_decode_attention.cu:257-265). */
+int pdattn_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream);
+
+/* Reads and rewrites `bytes` (a multiple of 16) of `buf` so that caches hold none of the data
+ * timed next; size it above the 256 MB Infinity Cache. No counterpart in the reference, which
+ * flushes with cudaMemsetAsync (common/bench.cuh:120, 159). */
+int pdattn_flush_cache(void* buf, size_t bytes, void* stream);
+
+typedef struct pdattn_device_info {
+    int  compute_units;
+    int  decode_wg_per_cu;     /* occupancy of the decode kernels (G = 4)  */
+    int  prefix_wg_per_cu;     /* occupancy of the MFMA prefix kernel      */
+    char arch[64];
+} pdattn_device_info;
+int pdattn_get_device_info(pdattn_device_info* info);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PDATTN_H */

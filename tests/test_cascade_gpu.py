@@ -1,0 +1,116 @@
+"""GPU parity of the shared-prefix (cascade) path against the fp64 oracle.
+
+Cases: the reference's cascade correctness cases (01_decode_attention.cu:782-787, seed 13,
+min_prefix 16, with the check that the detected prefix equals Lp at 01:796), the benchmark's
+cascade configuration (64 requests x 8192 shared + 512 private tokens), the prefix kernel on its
+own against per-chunk oracle partials, and the no-sharing fallback.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from _checks import check_lse, check_out
+from pdattn import inputs
+
+pytestmark = pytest.mark.gpu
+
+SCASES = [
+    (64, [1, 17, 40], 8, 8, "MHA prefix 64"),
+    (48, [5, 300, 33, 16, 2], 32, 8, "G=4 prefix 48 (partial tile)"),
+    (1024, [77] * 40, 32, 8, "G=4 40 seqs = 160 queries"),
+    (256, [100, 3], 16, 2, "G=8 prefix 256"),
+    (2048, [1] * 70, 32, 8, "G=4 280 queries (two query groups)"),
+]
+
+
+def _ref(bt, threads=8):
+    return oracle.decode(bt.q, bt.k, bt.v, bt.indptr, bt.indices, bt.last, bt.Hq, bt.Hkv,
+                         threads=threads)
+
+
+@pytest.mark.parametrize("dist", ["uniform", "normal"])
+@pytest.mark.parametrize("case", SCASES, ids=[c[4] for c in SCASES])
+def test_cascade_matches_oracle(case, dist):
+    import _gpu
+    Lp, suffix, Hq, Hkv, tag = case
+    print(f"[case] cascade {tag} dist={dist} seed=13", flush=True)
+    bt = inputs.make_shared_prefix_batch(Lp, suffix, Hq, Hkv, seed=13, dist=dist)
+    assert oracle.shared_prefix_pages(bt.indptr, bt.indices) * 16 == Lp
+    ro, rl = _ref(bt)
+    o, l, info = _gpu.run_cascade(_gpu.DeviceBatch(bt), min_prefix=16)
+    assert info.use == 1 and info.prefix_tokens == Lp
+    check_out(o, ro, tag=tag)
+    check_lse(l, rl, tag=tag)
+
+
+def test_cascade_benchmark_config():
+    """64 requests sharing an 8192-token prefix plus 512 private tokens each (config 5)."""
+    import _gpu
+    bt = inputs.make_shared_prefix_batch(8192, [512] * 64, 32, 8, seed=21)
+    print("[case] cascade 64 x (8192 + 512) seed=21", flush=True)
+    ro, rl = _ref(bt)
+    db = _gpu.DeviceBatch(bt)
+    o, l, info = _gpu.run_cascade(db)
+    assert info.use == 1 and info.prefix_tokens == 8192
+    check_out(o, ro, tag="cascade")
+    check_lse(l, rl, tag="cascade")
+    o2, l2, _ = _gpu.run_streamk(db)
+    check_out(o2, ro, tag="non-shared stream-K")
+    check_lse(l2, rl, tag="non-shared stream-K")
+
+
+@pytest.mark.parametrize("chunk_tokens", [16, 64, 96, 1024])
+def test_prefix_kernel_partials(chunk_tokens):
+    """The MFMA prefix kernel alone: per-chunk partials over the shared keys."""
+    import torch
+    import _gpu
+    import pdattn
+    Lp = 640
+    bt = inputs.make_shared_prefix_batch(Lp, [3, 20, 50], 32, 8, seed=8)
+    db = _gpu.DeviceBatch(bt)
+    nchunks = (Lp + chunk_tokens - 1) // chunk_tokens
+    rows = bt.B * bt.Hq
+    d = torch.device("cuda:0")
+    po = torch.full((rows, nchunks, 128), float("nan"), dtype=torch.float32, device=d)
+    pl = torch.full((rows, nchunks), float("nan"), dtype=torch.float32, device=d)
+    pp = pdattn.PrefixParams()
+    pp.q, pp.k_cache, pp.v_cache = db.q.data_ptr(), db.k.data_ptr(), db.v.data_ptr()
+    pp.prefix_pages = db.indices.data_ptr()          # sequence 0 starts at indptr[0] = 0
+    pp.part_o, pp.part_lse = po.data_ptr(), pl.data_ptr()
+    pp.B, pp.Hq, pp.Hkv = bt.B, bt.Hq, bt.Hkv
+    pp.prefix_len, pp.chunk_tokens, pp.part_stride = Lp, chunk_tokens, nchunks
+    pp.sm_scale = 1.0 / np.sqrt(128)
+    pdattn.cascade_prefix(pp)
+    torch.cuda.synchronize()
+    # oracle: per-chunk partials of a batch whose sequences are cut to the shared prefix
+    lens = [Lp] * bt.B
+    indptr = np.arange(bt.B + 1, dtype=np.int32) * (Lp // 16)
+    indices = np.concatenate([bt.indices[bt.indptr[b]:bt.indptr[b] + Lp // 16] for b in range(bt.B)])
+    last = np.full(bt.B, 16, np.int32)
+    ro, rl = oracle.partials(bt.q, bt.k, bt.v, indptr, indices, last, bt.Hq, bt.Hkv, nchunks, chunk_tokens)
+    check_lse(pl.cpu().numpy(), rl, tag="prefix part_lse")
+    check_out(po.cpu().numpy(), ro, tag="prefix part_o")
+    assert lens
+
+
+def test_unshared_batch_falls_back():
+    """No shared pages: the plan reports use = 0 and the result equals plain decode
+    (01_decode_attention.cu:810-815)."""
+    import _gpu
+    bt = inputs.make_batch([1000] * 4, 32, 8, seed=3)
+    assert oracle.shared_prefix_pages(bt.indptr, bt.indices) == 0
+    ro, rl = _ref(bt)
+    o, l, info = _gpu.run_cascade(_gpu.DeviceBatch(bt), min_prefix=16)
+    assert info.use == 0
+    check_out(o, ro, tag="fallback")
+    check_lse(l, rl, tag="fallback")
+
+
+def test_short_prefix_below_min_prefix_falls_back():
+    import _gpu
+    bt = inputs.make_shared_prefix_batch(32, [10, 20], 8, 2, seed=3)
+    ro, rl = _ref(bt)
+    o, l, info = _gpu.run_cascade(_gpu.DeviceBatch(bt), min_prefix=256)
+    assert info.use == 0
+    check_out(o, ro)
+    check_lse(l, rl)
