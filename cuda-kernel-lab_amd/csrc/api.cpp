@@ -10,6 +10,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -163,12 +164,12 @@ int ensure_ws(pdattn_workspace* ws, size_t need) {
 
 struct pdattn_plan {
     int B = 0, Hq = 0, Hkv = 0, G = 0;
-    int nnz = 0, jbase = 0, W = 1, n_empty = 0, b_first = 0;
+    int nnz = 0, jbase = 0, W = 1, n_empty = 0;
     int64_t U = 0;
     int split_pairs = 0, max_contrib = 0;
     // workspace layout (bytes from the base)
     size_t off_desc = 0, off_empty = 0, off_cnt = 0, off_plse = 0, off_po = 0, ws_bytes = 0;
-    std::vector<int32_t> host_blob;   // desc_b0[W] followed by empty_seq[n_empty]
+    std::vector<int32_t> host_blob;   // desc[W * kDescInts] followed by empty_seq[n_empty]
     void* pinned = nullptr;           // pinned copy of host_blob for stream-ordered upload
     size_t blob_bytes = 0;
     const void* uploaded_to = nullptr;
@@ -190,6 +191,11 @@ struct pdattn_cascade_plan {
 namespace {
 
 // Balanced split of the flattened (kv head, page) units over W workgroups; see pdattn.h.
+// Units are pages in kv-head-major order: unit u is page-table position (u mod nnz) of kv head
+// (u / nnz). Workgroup w owns units [U w / W, U (w+1) / W). The walk below cuts each range into
+// segments at sequence boundaries and records, per segment, everything the kernel needs, so the
+// kernel never reads kv_indptr / kv_last_page_len. W grows (doubling) until every workgroup has
+// at most kSegMax segments and kRangeMax pages.
 int build_streamk_plan(const int32_t* indptr, const int32_t* last, int B, int Hq, int Hkv,
                        int force_wg, pdattn_plan* pl) {
     int G = 0;
@@ -206,12 +212,8 @@ int build_streamk_plan(const int32_t* indptr, const int32_t* last, int B, int Hq
     pl->nnz = B > 0 ? indptr[B] - indptr[0] : 0;
     pl->U = (int64_t)Hkv * pl->nnz;
     std::vector<int32_t> empty;
-    pl->b_first = -1;
-    for (int b = 0; b < B; ++b) {
+    for (int b = 0; b < B; ++b)
         if (indptr[b + 1] == indptr[b]) empty.push_back(b);
-        else if (pl->b_first < 0) pl->b_first = b;
-    }
-    if (pl->b_first < 0) pl->b_first = 0;
     pl->n_empty = (int)empty.size();
 
     // grid: one full wave of resident workgroups (runtime occupancy x CUs), never more
@@ -223,48 +225,70 @@ int build_streamk_plan(const int32_t* indptr, const int32_t* last, int B, int Hq
         W = (int64_t)f.cus * std::max(1, f.occ_streamk[G]);
         if (pl->U == 0) W = std::min<int64_t>(W, f.cus);
     }
-    if (pl->U == 0) W = std::max<int64_t>(1, std::min<int64_t>(W, (int64_t)pl->n_empty * Hq));
+    if (pl->U == 0) W = std::max<int64_t>(1, std::min<int64_t>(W, (int64_t)pl->n_empty * Hkv));
     else W = std::max<int64_t>(1, std::min<int64_t>(W, pl->U));
-    if (W > (1 << 30)) return fail(PDATTN_ERR_INVALID_ARGUMENT, "grid too large");
-    pl->W = (int)W;
+    W = std::max<int64_t>(W, (pl->U + kRangeMax - 1) / kRangeMax);
+    if (W > (1 << 28)) return fail(PDATTN_ERR_INVALID_ARGUMENT, "grid too large");
 
-    // desc_b0[w]: the sequence holding the first page of workgroup w's range
-    std::vector<int32_t> desc(pl->W, 0);
-    if (pl->U > 0) {
-        for (int w = 0; w < pl->W; ++w) {
-            const int64_t u0 = pl->U * w / pl->W;
-            const int j = (int)(u0 % pl->nnz);
-            // first b with indptr[b+1] - jbase > j
-            const int32_t* it = std::upper_bound(indptr + 1, indptr + B + 1, j + pl->jbase);
-            desc[w] = (int)(it - (indptr + 1));
-        }
-        // contributor statistics
+    const int64_t U = pl->U, nnz = pl->nnz;
+    auto seq_len = [&](int b) { return (indptr[b + 1] - indptr[b] - 1) * kPage + last[b]; };
+    std::vector<int32_t> desc;
+    for (;;) {
+        desc.assign((size_t)W * kDescInts, 0);
+        bool ok = true;
         int split = 0, mx = 1;
-        for (int kvh = 0; kvh < Hkv; ++kvh)
-            for (int b = 0; b < B; ++b) {
+        for (int64_t w = 0; w < W && ok && U > 0; ++w) {
+            const int64_t u0 = U * w / W, u1 = U * (w + 1) / W;
+            if (u1 - u0 > kRangeMax) { ok = false; break; }
+            int32_t* d = &desc[(size_t)w * kDescInts];
+            int nseg = 0;
+            for (int64_t u = u0; u < u1;) {
+                const int kvh = (int)(u / nnz);
+                const int j = (int)(u % nnz);
+                // the non-empty sequence holding position j: first b with indptr[b+1] - jbase > j
+                const int b = (int)(std::upper_bound(indptr + 1, indptr + B + 1, j + pl->jbase) - (indptr + 1));
                 const int pb = indptr[b] - pl->jbase, pe = indptr[b + 1] - pl->jbase;
-                if (pe == pb) continue;
-                const int64_t uf = (int64_t)kvh * pl->nnz + pb, ul = (int64_t)kvh * pl->nnz + pe - 1;
-                const int64_t w1 = ((uf + 1) * pl->W - 1) / pl->U, w2 = ((ul + 1) * pl->W - 1) / pl->U;
-                if (w2 > w1) ++split;
-                mx = std::max<int>(mx, (int)(w2 - w1 + 1));
+                const int64_t seg_end = std::min<int64_t>(u1, (int64_t)kvh * nnz + pe);
+                if (nseg == kSegMax) { ok = false; break; }
+                const int64_t uf = (int64_t)kvh * nnz + pb, ul = uf + (pe - pb) - 1;
+                const int64_t w1 = ((uf + 1) * W - 1) / U, w2 = ((ul + 1) * W - 1) / U;
+                int32_t* sg = d + 8 + kSegInts * nseg;
+                sg[0] = b;
+                sg[1] = kvh;
+                sg[2] = (int)(u - u0);
+                sg[3] = (int)(seg_end - u);
+                sg[4] = (j - pb) * kPage;
+                sg[5] = (seg_end - (int64_t)kvh * nnz == pe) ? seq_len(b) : (int)(seg_end - (int64_t)kvh * nnz - pb) * kPage;
+                sg[6] = (int)w1;
+                sg[7] = (int)(w2 - w1 + 1);
+                if (w == w1 && w2 > w1) ++split;
+                mx = std::max(mx, (int)(w2 - w1 + 1));
+                ++nseg;
+                u = seg_end;
             }
-        pl->split_pairs = split;
-        pl->max_contrib = mx;
+            d[0] = nseg;
+        }
+        if (ok) {
+            pl->split_pairs = split;
+            pl->max_contrib = mx;
+            break;
+        }
+        if (W >= U) return fail(PDATTN_ERR_INVALID_ARGUMENT, "cannot partition the batch");
+        W = std::min<int64_t>(U, W * 2);
     }
+    pl->W = (int)W;
     pl->host_blob = desc;
     pl->host_blob.insert(pl->host_blob.end(), empty.begin(), empty.end());
 
     const size_t pairs = (size_t)B * Hkv;
     const size_t slots = pairs + (size_t)pl->W;
     size_t off = 0;
-    pl->off_desc = off;  off += align_up(sizeof(int32_t) * pl->W);
+    pl->off_desc = off;  off += align_up(sizeof(int32_t) * desc.size());
     pl->off_empty = off; off += align_up(sizeof(int32_t) * std::max(1, pl->n_empty));
     pl->off_cnt = off;   off += align_up(sizeof(int32_t) * std::max<size_t>(1, pairs));
     pl->off_plse = off;  off += align_up(sizeof(float) * slots * G);
     pl->off_po = off;    off += align_up(sizeof(float) * slots * G * kHeadDim);
     pl->ws_bytes = off;
-
     pl->blob_bytes = sizeof(int32_t) * pl->host_blob.size();
     return PDATTN_OK;
 }
@@ -281,7 +305,7 @@ int upload_streamk(pdattn_plan* pl, void* ws, size_t bytes, hipStream_t s) {
     if (bytes < pl->ws_bytes)
         return fail(PDATTN_ERR_WORKSPACE, "workspace holds %zu bytes, plan needs %zu", bytes, pl->ws_bytes);
     char* base = static_cast<char*>(ws);
-    const size_t desc_bytes = sizeof(int32_t) * pl->W;
+    const size_t desc_bytes = sizeof(int32_t) * (size_t)pl->W * kDescInts;
     if (pl->blob_bytes && !pl->pinned) {
         // pinned staging copy, made once: the copy below is stream-ordered and asynchronous
         hipError_t e = hipHostMalloc(&pl->pinned, pl->blob_bytes, hipHostMallocDefault);
@@ -319,12 +343,10 @@ int run_streamk(const pdattn_plan* pl, const void* q, const void* k, const void*
     a.q = static_cast<const _Float16*>(q);
     a.k = static_cast<const uint8_t*>(k);
     a.v = static_cast<const uint8_t*>(v);
-    a.kv_indptr = indptr;
     a.kv_indices = indices;
-    a.kv_last = last;
     a.out = static_cast<_Float16*>(out);
     a.lse = lse;
-    a.desc_b0 = reinterpret_cast<const int32_t*>(base + pl->off_desc);
+    a.desc = reinterpret_cast<const int32_t*>(base + pl->off_desc);
     a.empty_seq = reinterpret_cast<const int32_t*>(base + pl->off_empty);
     a.counters = reinterpret_cast<int32_t*>(base + pl->off_cnt);
     a.part_lse = reinterpret_cast<float*>(base + pl->off_plse);
@@ -332,7 +354,6 @@ int run_streamk(const pdattn_plan* pl, const void* q, const void* k, const void*
     a.extra_o = extra_o;
     a.extra_lse = extra_lse;
     a.n_extra = n_extra;
-    a.extra_stride = n_extra;
     a.U = pl->U;
     a.nnz = pl->nnz;
     a.jbase = pl->jbase;
@@ -341,7 +362,6 @@ int run_streamk(const pdattn_plan* pl, const void* q, const void* k, const void*
     a.Hkv = pl->Hkv;
     a.W = pl->W;
     a.n_empty = pl->n_empty;
-    a.b_first = pl->b_first;
     a.scale_log2 = sm_scale * 1.4426950408889634f;
     PD_HIP(launch_decode_streamk(a, pl->G, s));
     return PDATTN_OK;
@@ -727,7 +747,7 @@ int pdattn_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stre
     if (bytes == 0) return PDATTN_OK;
     DeviceFacts f;
     if (int st = device_facts(&f)) return st;
-    PD_HIP(launch_stream_read(buf, bytes, sink, f.cus * 16, static_cast<hipStream_t>(stream)));
+    PD_HIP(launch_stream_read(buf, bytes, sink, f.cus, static_cast<hipStream_t>(stream)));
     return PDATTN_OK;
 }
 

@@ -109,8 +109,8 @@ __global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
             kst[i] = u32x4{0u, 0u, 0u, 0u};
             if (key < kend) {
                 const size_t pid = (uint32_t)sm.pg[(key - kbeg) >> 4];
-                kst[i] = *reinterpret_cast<const u32x4*>(a.k + pid * page_bytes +
-                                                         (size_t)(((key & 15) * a.Hkv + kvh) * 256 + sc * 16));
+                kst[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+                    a.k + pid * page_bytes + (size_t)(((key & 15) * a.Hkv + kvh) * 256 + sc * 16)));
             }
         }
 #pragma unroll
@@ -119,8 +119,8 @@ __global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
             vst[i] = u32x4{0u, 0u, 0u, 0u};
             if (key < kend) {
                 const size_t pid = (uint32_t)sm.pg[(key - kbeg) >> 4];
-                vst[i] = *reinterpret_cast<const u32x4*>(a.v + pid * page_bytes +
-                                                         (size_t)(((key & 15) * a.Hkv + kvh) * 256 + sc * 16));
+                vst[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+                    a.v + pid * page_bytes + (size_t)(((key & 15) * a.Hkv + kvh) * 256 + sc * 16)));
             }
         }
     };

@@ -32,6 +32,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <cstdlib>
 
 #include "pdattn_internal.h"
 
@@ -43,12 +44,15 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.69314718055994531f;
-constexpr int NW = kDecodeWaves;
-constexpr int NT = kDecodeThreads;
 
-template <int G>
-struct Geo {
-    static constexpr int LPR = (G >= 8) ? 16 : 8;  // lanes per 256-byte K/V row
+// Compile-time shape of a decode kernel instance.
+template <int G_, int LPR_, int NW_, int NBUF_>
+struct Cfg {
+    static constexpr int G = G_;                   // query heads per kv head
+    static constexpr int LPR = LPR_;               // lanes per 256-byte K/V row (8 or 16)
+    static constexpr int NW = NW_;                 // waves per workgroup
+    static constexpr int NBUF = NBUF_;             // pages held in VGPRs per wave (NBUF-1 in flight)
+    static constexpr int NT = NW * 64;
     static constexpr int RPI = 64 / LPR;           // rows per wave-wide load
     static constexpr int PPL = 16 / LPR;           // 16-byte pieces per lane per row
     static constexpr int RG = kPage / RPI;         // rows of each page held by one lane
@@ -78,49 +82,55 @@ __device__ __forceinline__ f16x2 as_h2(uint32_t w) { return __builtin_bit_cast(f
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 
-template <int G>
+template <class C>
 struct WaveState {
-    float m[G];                   // running max, log2 units
-    float l[G];                   // running sum of 2^(x - m)
-    float o[G][Geo<G>::DPL];      // running unnormalized output slice
+    float m[C::G];                // running max, log2 units
+    float l[C::G];                // running sum of 2^(x - m)
+    float o[C::G][C::DPL];        // running unnormalized output slice
 };
 
-template <int G>
+template <class C>
 struct PageRegs {
-    u32x4 k[Geo<G>::RG][Geo<G>::PPL];
-    u32x4 v[Geo<G>::RG][Geo<G>::PPL];
+    u32x4 k[C::RG][C::PPL];
+    u32x4 v[C::RG][C::PPL];
 };
 
-template <int G>
+template <int G, int NW>
 struct Smem {
     float m[NW][G];
     float l[NW][G];
     float o[NW][G][kHeadDim];
     float fo[G][kHeadDim];    // combined, normalized output of the workgroup
     float flse[G];            // combined lse (natural log)
+    float wmax[NW][G];        // merge scratch: per-wave maxima,
+    float gmax[G];            //   per-row maximum,
+    float red[NW * 64 * 6];   //   per-thread partial states
 };
 
-template <int G>
-__device__ __forceinline__ void load_page(PageRegs<G>& pr, const uint8_t* kp, const uint8_t* vp,
+template <class C>
+__device__ __forceinline__ void load_page(PageRegs<C>& pr, const uint8_t* kp, const uint8_t* vp,
                                           uint32_t lbase, uint32_t rstride) {
-    using g = Geo<G>;
+    using g = C;
 #pragma unroll
     for (int i = 0; i < g::RG; ++i)
 #pragma unroll
         for (int kk = 0; kk < g::PPL; ++kk) {
             const uint32_t off = lbase + i * rstride + kk * (g::LPR * 16);
-            pr.k[i][kk] = *reinterpret_cast<const u32x4*>(kp + off);
-            pr.v[i][kk] = *reinterpret_cast<const u32x4*>(vp + off);
+            // K/V bytes are read exactly once: non-temporal loads keep them from displacing
+            // reusable lines in L2 and the Infinity Cache
+            pr.k[i][kk] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + off));
+            pr.v[i][kk] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vp + off));
         }
 }
 
 // One page: scores, online-softmax update, PV accumulation. tok_r is the token index of this
 // lane's row in row group 0; keys outside [tb, te) are masked.
-template <int G>
-__device__ __forceinline__ void page_step(WaveState<G>& st, const PageRegs<G>& pr,
-                                          const f16x2 (&qv)[G][Geo<G>::PPL][4], int tok_r,
+template <class C>
+__device__ __forceinline__ void page_step(WaveState<C>& st, const PageRegs<C>& pr,
+                                          const f16x2 (&qv)[C::G][C::PPL][4], int tok_r,
                                           int tb, int te, float scale2) {
-    using g = Geo<G>;
+    using g = C;
+    constexpr int G = C::G;
     float x[g::RG][G];
 #pragma unroll
     for (int i = 0; i < g::RG; ++i) {
@@ -180,14 +190,16 @@ __device__ __forceinline__ void page_step(WaveState<G>& st, const PageRegs<G>& p
     }
 }
 
-// Attention of the G query heads of (b, kvh) over keys [t0, t1) of one sequence whose page list
-// starts at `pages`. Leaves the normalized output in sm.fo and the lse in sm.flse (all threads
-// of the workgroup must call it; it ends with a barrier).
-template <int G>
-__device__ __forceinline__ void process_range(Smem<G>& sm, const _Float16* qrow, const uint8_t* kbase,
-                              const uint8_t* vbase, const int32_t* pages, int t0, int t1,
+// Attention of the G query heads of (b, kvh) over keys [t0, t1) of one sequence. pages[i] is the
+// physical page holding tokens [tok_base + 16 i, tok_base + 16 i + 16) (global memory or LDS).
+// Leaves the normalized output in sm.fo and the lse in sm.flse (all threads of the workgroup
+// must call it; it ends with a barrier).
+template <class C>
+__device__ __forceinline__ void process_range(Smem<C::G, C::NW>& sm, const _Float16* qrow, const uint8_t* kbase,
+                              const uint8_t* vbase, const int32_t* pages, int tok_base, int t0, int t1,
                               int Hkv, int kvh, float scale2) {
-    using g = Geo<G>;
+    using g = C;
+    constexpr int G = C::G, NW = C::NW, NBUF = C::NBUF;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int r = lane / g::LPR, c = lane % g::LPR;
 
@@ -202,7 +214,7 @@ __device__ __forceinline__ void process_range(Smem<G>& sm, const _Float16* qrow,
             for (int e = 0; e < 4; ++e) qv[h][kk][e] = as_h2(raw[e]);
         }
 
-    WaveState<G> st;
+    WaveState<C> st;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
         st.m[h] = -INFINITY;
@@ -212,7 +224,7 @@ __device__ __forceinline__ void process_range(Smem<G>& sm, const _Float16* qrow,
     }
 
     if (t1 > t0) {
-        const int pfirst = t0 / kPage, plast = (t1 - 1) / kPage;
+        const int pfirst = (t0 - tok_base) / kPage, plast = (t1 - 1 - tok_base) / kPage;
         const int npg = plast - pfirst + 1;
         const int nmine = npg > wave ? (npg - wave + NW - 1) / NW : 0;
         const size_t page_bytes = (size_t)kPage * Hkv * 256;
@@ -222,26 +234,28 @@ __device__ __forceinline__ void process_range(Smem<G>& sm, const _Float16* qrow,
             const int cnt = min(64, nmine - base);
             // lane j holds the physical page of this wave's (base + j)-th page
             const int pidv = lane < cnt ? pages[pfirst + wave + NW * (base + lane)] : 0;
-            PageRegs<G> A, Bf;
-            {
-                const size_t pid = (uint32_t)__builtin_amdgcn_readlane(pidv, 0);
-                load_page<G>(A, kbase + pid * page_bytes, vbase + pid * page_bytes, lbase, rstride);
+            // ring of NBUF pages in VGPRs: page i lives in buf[i % NBUF]; NBUF-1 are in flight
+            // while one is computed. Past the end the last page is loaded again (an L2 hit), so
+            // every iteration issues the same loads and the wait counts stay exact.
+            PageRegs<C> buf[NBUF];
+#pragma unroll
+            for (int u = 0; u < NBUF - 1; ++u) {
+                const size_t pid = (uint32_t)__builtin_amdgcn_readlane(pidv, min(u, cnt - 1));
+                load_page<C>(buf[u], kbase + pid * page_bytes, vbase + pid * page_bytes, lbase, rstride);
             }
-            for (int it = 0; it < cnt; it += 2) {
-                {
-                    // prefetch page it+1 (the last page again when there is none: an L2 hit)
-                    const int nx = min(it + 1, cnt - 1);
-                    const size_t pid = (uint32_t)__builtin_amdgcn_readlane(pidv, nx);
-                    load_page<G>(Bf, kbase + pid * page_bytes, vbase + pid * page_bytes, lbase, rstride);
+            for (int it = 0; it < cnt; it += NBUF) {
+#pragma unroll
+                for (int u = 0; u < NBUF; ++u) {
+                    if (it + u >= cnt) break;
+                    {
+                        const int nx = min(it + u + NBUF - 1, cnt - 1);
+                        const size_t pid = (uint32_t)__builtin_amdgcn_readlane(pidv, nx);
+                        load_page<C>(buf[(u + NBUF - 1) % NBUF], kbase + pid * page_bytes,
+                                     vbase + pid * page_bytes, lbase, rstride);
+                    }
+                    page_step<C>(st, buf[u], qv, tok_base + (pfirst + wave + NW * (base + it + u)) * kPage + r,
+                                 t0, t1, scale2);
                 }
-                page_step<G>(st, A, qv, (pfirst + wave + NW * (base + it)) * kPage + r, t0, t1, scale2);
-                if (it + 1 >= cnt) break;
-                {
-                    const int nx = min(it + 2, cnt - 1);
-                    const size_t pid = (uint32_t)__builtin_amdgcn_readlane(pidv, nx);
-                    load_page<G>(A, kbase + pid * page_bytes, vbase + pid * page_bytes, lbase, rstride);
-                }
-                page_step<G>(st, Bf, qv, (pfirst + wave + NW * (base + it + 1)) * kPage + r, t0, t1, scale2);
             }
         }
     }
@@ -282,7 +296,7 @@ __device__ __forceinline__ void process_range(Smem<G>& sm, const _Float16* qrow,
         }
     }
     __syncthreads();
-    for (int idx = tid; idx < G * kHeadDim; idx += NT) {
+    for (int idx = tid; idx < G * kHeadDim; idx += NW * 64) {
         const int h = idx / kHeadDim, d = idx % kHeadDim;
         float M = -INFINITY;
 #pragma unroll
@@ -300,10 +314,145 @@ __device__ __forceinline__ void process_range(Smem<G>& sm, const _Float16* qrow,
     __syncthreads();
 }
 
+
+// Kernel arguments of the balanced kernel read in place from the kernarg segment. The pointer is
+// laundered through an empty asm statement at every use, so the compiler reloads those fields
+// (scalar loads, cached) where they are needed instead of holding them in SGPRs across the page
+// loop, where they would spill. The kernarg-segment intrinsic is only valid in the kernel body
+// itself (in a called function it evaluates to null), so kargs() is called only from the kernel
+// and the pointer is passed down to the (force-inlined) helpers.
+typedef const __attribute__((address_space(4))) StreamKArgs* KArgPtr;
+__device__ __forceinline__ KArgPtr kargs() {
+    KArgPtr p = (KArgPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(p));
+    return p;
+}
+
+// ---- merging partial states ----------------------------------------------------------------
+// Online log-sum-exp accumulation of one partial state (lse l, normalized output o) into
+// (m, ws, acc): acc / ws is the merged output, m + ln ws the merged lse. Empty states
+// (l = -inf) are identities.
+__device__ __forceinline__ void lse_accumulate(float& m, float& ws, float4& acc, float l, float4 o) {
+    if (l == -INFINITY) return;
+    if (l > m) {
+        const float sc = fast_exp2((m - l) * kLog2e);   // m = -inf gives 0
+        ws *= sc;
+        acc.x *= sc;
+        acc.y *= sc;
+        acc.z *= sc;
+        acc.w *= sc;
+        m = l;
+    }
+    const float w = fast_exp2((l - m) * kLog2e);
+    ws += w;
+    acc.x = fmaf(w, o.x, acc.x);
+    acc.y = fmaf(w, o.y, acc.y);
+    acc.z = fmaf(w, o.z, acc.z);
+    acc.w = fmaf(w, o.w, acc.w);
+}
+
+// Log-sum-exp merge of the G rows of one (sequence, kv head) pair from a list of sources, in a
+// fixed source order (deterministic whatever order the sources were produced in):
+//   source 0 (if `own`): the workgroup's own result in LDS (sm.fo / sm.flse);
+//   then `nslots` stored partials: o at part_o[((s0 + k) * G + h) * 128], lse at part_lse[(s0 + k) * G + h];
+//   then the `n_extra` extra partials of each row: o at extra_o[(row * n_extra + e) * 128], lse at
+//   extra_lse[row * n_extra + e].
+// One pass: each thread owns one 4-dim quad of one row and every TPQ-th source, issues all its
+// loads, accumulates them online, and the TPQ partial states of a quad are combined in order
+// through LDS. Writes fp16 out and fp32 lse; a row whose every source is empty gets 0 / -inf.
+template <int G, int NW, bool ATOMIC_LOADS>
+__device__ __forceinline__ void merge_sources(Smem<G, NW>& sm, KArgPtr a, int b, int kvh, bool own,
+                                              int64_t s0, int nslots) {
+    constexpr int NT = NW * 64;
+    constexpr int Q = G * 32;          // 4-dim quads of the G rows
+    constexpr int TPQ = NT / Q;        // threads per quad
+    static_assert(NT % Q == 0, "thread count must cover the quads");
+    const int tid = threadIdx.x;
+    const int n_extra = a->n_extra;
+    const int nsrc = (own ? 1 : 0) + nslots + n_extra;
+    const size_t row0 = (size_t)b * a->Hq + (size_t)kvh * G;
+    const int quad = tid % Q, r = tid / Q;
+    const int h = quad / 32, d0 = 4 * (quad % 32);
+
+    auto load_src = [&](int k, float& l, float4& o) {
+        if (own) {
+            if (k == 0) {
+                l = sm.flse[h];
+                o = make_float4(sm.fo[h][d0], sm.fo[h][d0 + 1], sm.fo[h][d0 + 2], sm.fo[h][d0 + 3]);
+                return;
+            }
+            --k;
+        }
+        if (k < nslots) {
+            const float* pl = a->part_lse + (s0 + k) * G + h;
+            const float* po = a->part_o + ((s0 + k) * G + h) * kHeadDim + d0;
+            if constexpr (ATOMIC_LOADS) {
+                l = __hip_atomic_load(pl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                o = make_float4(__hip_atomic_load(po, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                                __hip_atomic_load(po + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                                __hip_atomic_load(po + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                                __hip_atomic_load(po + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            } else {
+                l = *pl;
+                o = *reinterpret_cast<const float4*>(po);
+            }
+            return;
+        }
+        const size_t e = (row0 + h) * n_extra + (k - nslots);
+        l = a->extra_lse[e];
+        o = *reinterpret_cast<const float4*>(a->extra_o + e * kHeadDim + d0);
+    };
+
+    float m = -INFINITY, ws = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = r; k < nsrc; k += 4 * TPQ) {
+        float l[4];
+        float4 o[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) load_src(min(k + u * TPQ, nsrc - 1), l[u], o[u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (k + u * TPQ < nsrc) lse_accumulate(m, ws, acc, l[u], o[u]);
+    }
+    float* red = sm.red + (size_t)tid * 6;
+    red[0] = m;
+    red[1] = ws;
+    red[2] = acc.x;
+    red[3] = acc.y;
+    red[4] = acc.z;
+    red[5] = acc.w;
+    __syncthreads();
+    if (r == 0) {
+        for (int rr = 1; rr < TPQ; ++rr) {
+            const float* o = sm.red + (size_t)(rr * Q + quad) * 6;
+            if (o[1] > 0.f) {
+                // fold in a partial state (o[0] + ln o[1], o[2..5] / o[1])
+                const float mm = fmaxf(m, o[0]);
+                const float sa = fast_exp2((m - mm) * kLog2e), sb = fast_exp2((o[0] - mm) * kLog2e);
+                ws = ws * sa + o[1] * sb;
+                acc.x = acc.x * sa + o[2] * sb;
+                acc.y = acc.y * sa + o[3] * sb;
+                acc.z = acc.z * sa + o[4] * sb;
+                acc.w = acc.w * sa + o[5] * sb;
+                m = mm;
+            }
+        }
+        const float inv = ws > 0.f ? 1.f / ws : 0.f;
+        _Float16* out = a->out + (row0 + h) * kHeadDim + d0;
+        out[0] = (_Float16)(acc.x * inv);
+        out[1] = (_Float16)(acc.y * inv);
+        out[2] = (_Float16)(acc.z * inv);
+        out[3] = (_Float16)(acc.w * inv);
+        if (d0 == 0) a->lse[row0 + h] = ws > 0.f ? m + fast_log2(ws) * kLn2 : -INFINITY;
+    }
+    __syncthreads();
+}
+
 // ---- uniform chunks: the reference's decode_partial launch shape -------------------------
-template <int G>
-__global__ __launch_bounds__(NT) void decode_partial_kernel(PartialArgs a) {
-    __shared__ Smem<G> sm;
+template <class C>
+__global__ __launch_bounds__(C::NT) void decode_partial_kernel(PartialArgs a) {
+    constexpr int G = C::G;
+    __shared__ Smem<G, C::NW> sm;
     const int chunk = blockIdx.x;
     const int b = blockIdx.y / a.Hkv, kvh = blockIdx.y % a.Hkv;
     const int pb = a.kv_indptr[b];
@@ -311,9 +460,9 @@ __global__ __launch_bounds__(NT) void decode_partial_kernel(PartialArgs a) {
     const int len = np > 0 ? (np - 1) * kPage + a.kv_last[b] : 0;
     const int kbeg = a.kv_start + chunk * a.chunk_tokens;
     const int kend = min(len, kbeg + a.chunk_tokens);
-    process_range<G>(sm, a.q + ((size_t)b * a.Hq + kvh * G) * kHeadDim, a.k, a.v,
-                     a.kv_indices + pb, kbeg, kend, a.Hkv, kvh, a.scale_log2);
-    for (int idx = threadIdx.x; idx < G * kHeadDim; idx += NT) {
+    process_range<C>(sm, a.q + ((size_t)b * a.Hq + kvh * G) * kHeadDim, a.k, a.v,
+                     a.kv_indices + pb, 0, kbeg, kend, a.Hkv, kvh, a.scale_log2);
+    for (int idx = threadIdx.x; idx < G * kHeadDim; idx += C::NT) {
         const int h = idx / kHeadDim, d = idx % kHeadDim;
         const size_t slot = ((size_t)b * a.Hq + kvh * G + h) * a.part_stride + a.chunk_base + chunk;
         a.part_o[slot * kHeadDim + d] = sm.fo[h][d];
@@ -322,150 +471,142 @@ __global__ __launch_bounds__(NT) void decode_partial_kernel(PartialArgs a) {
 }
 
 // ---- log-sum-exp merge: the reference's merge_states launch shape -------------------------
-__global__ __launch_bounds__(kHeadDim) void merge_states_kernel(const float* __restrict__ part_o,
-                                                                 const float* __restrict__ part_lse,
-                                                                 _Float16* __restrict__ out,
-                                                                 float* __restrict__ lse_out,
-                                                                 int num_chunks) {
-    const int row = blockIdx.x, t = threadIdx.x;
+// One workgroup per row: each of 8 threads per 4-dim quad takes every 8th chunk (independent
+// 16-byte loads, accumulated online), and the 8 states are combined in order through LDS.
+constexpr int kMergeThreads = 256;
+__global__ __launch_bounds__(kMergeThreads) void merge_states_kernel(const float* __restrict__ part_o,
+                                                                      const float* __restrict__ part_lse,
+                                                                      _Float16* __restrict__ out,
+                                                                      float* __restrict__ lse_out,
+                                                                      int num_chunks) {
+    constexpr int Q = kHeadDim / 4, TPQ = kMergeThreads / Q;
+    __shared__ float red[kMergeThreads * 6];
+    const int row = blockIdx.x, tid = threadIdx.x;
     const float* pl = part_lse + (size_t)row * num_chunks;
-    float m = -INFINITY;
-    for (int c = 0; c < num_chunks; ++c) m = fmaxf(m, pl[c]);
-    float ws = 0.f, acc = 0.f;
-    if (m != -INFINITY) {
-        const float* po = part_o + (size_t)row * num_chunks * kHeadDim + t;
-        for (int c = 0; c < num_chunks; ++c) {
-            const float w = fast_exp2((pl[c] - m) * kLog2e);
-            ws += w;
-            acc = fmaf(w, po[(size_t)c * kHeadDim], acc);
+    const float* po = part_o + (size_t)row * num_chunks * kHeadDim;
+    const int quad = tid % Q, r = tid / Q, d0 = 4 * quad;
+    float m = -INFINITY, ws = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int c = r; c < num_chunks; c += 4 * TPQ) {
+        float l[4];
+        float4 o[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int cc = min(c + u * TPQ, num_chunks - 1);
+            l[u] = pl[cc];
+            o[u] = *reinterpret_cast<const float4*>(po + (size_t)cc * kHeadDim + d0);
         }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            if (c + u * TPQ < num_chunks) lse_accumulate(m, ws, acc, l[u], o[u]);
     }
-    out[(size_t)row * kHeadDim + t] = (_Float16)(ws > 0.f ? acc / ws : 0.f);
-    if (t == 0) lse_out[row] = ws > 0.f ? m + fast_log2(ws) * kLn2 : -INFINITY;
+    float* rd = red + tid * 6;
+    rd[0] = m;
+    rd[1] = ws;
+    rd[2] = acc.x;
+    rd[3] = acc.y;
+    rd[4] = acc.z;
+    rd[5] = acc.w;
+    __syncthreads();
+    if (r == 0) {
+        for (int rr = 1; rr < TPQ; ++rr) {
+            const float* o = red + (rr * Q + quad) * 6;
+            if (o[1] > 0.f) {
+                const float mm = fmaxf(m, o[0]);
+                const float sa = fast_exp2((m - mm) * kLog2e), sb = fast_exp2((o[0] - mm) * kLog2e);
+                ws = ws * sa + o[1] * sb;
+                acc.x = acc.x * sa + o[2] * sb;
+                acc.y = acc.y * sa + o[3] * sb;
+                acc.z = acc.z * sa + o[4] * sb;
+                acc.w = acc.w * sa + o[5] * sb;
+                m = mm;
+            }
+        }
+        const float inv = ws > 0.f ? 1.f / ws : 0.f;
+        _Float16* op = out + (size_t)row * kHeadDim + d0;
+        op[0] = (_Float16)(acc.x * inv);
+        op[1] = (_Float16)(acc.y * inv);
+        op[2] = (_Float16)(acc.z * inv);
+        op[3] = (_Float16)(acc.w * inv);
+        if (quad == 0) lse_out[row] = ws > 0.f ? m + fast_log2(ws) * kLn2 : -INFINITY;
+    }
 }
 
 // ---- balanced single launch ------------------------------------------------------------------
-// Combines `n` stored partial states (natural-log lse) of one row plus the row's extra partials,
-// in fixed order, and writes fp16 out / fp32 lse. `own_o/own_lse` (if own_valid) is one more
-// state taken from LDS, placed first.
-template <int G>
-__device__ __forceinline__ void combine_row(const StreamKArgs& a, size_t row, int h, int d,
-                                            bool own_valid, float own_o, float own_lse,
-                                            const float* slot_o, const float* slot_lse,
-                                            int nslots) {
-    float m = own_valid ? own_lse : -INFINITY;
-    for (int k = 0; k < nslots; ++k) m = fmaxf(m, slot_lse[(size_t)k * G]);
-    const float* eo = a.extra_o + row * (size_t)a.extra_stride * kHeadDim;
-    const float* el = a.extra_lse + row * (size_t)a.extra_stride;
-    for (int e = 0; e < a.n_extra; ++e) m = fmaxf(m, el[e]);
-    float ws = 0.f, acc = 0.f;
-    if (m != -INFINITY) {
-        if (own_valid && own_lse != -INFINITY) {
-            const float w = fast_exp2((own_lse - m) * kLog2e);
-            ws += w;
-            acc = fmaf(w, own_o, acc);
-        }
-        for (int k = 0; k < nslots; ++k) {
-            const float lk = slot_lse[(size_t)k * G];
-            if (lk == -INFINITY) continue;
-            const float w = fast_exp2((lk - m) * kLog2e);
-            ws += w;
-            acc = fmaf(w, slot_o[(size_t)k * G * kHeadDim], acc);
-        }
-        for (int e = 0; e < a.n_extra; ++e) {
-            if (el[e] == -INFINITY) continue;
-            const float w = fast_exp2((el[e] - m) * kLog2e);
-            ws += w;
-            acc = fmaf(w, eo[(size_t)e * kHeadDim + d], acc);
-        }
-    }
-    a.out[row * kHeadDim + d] = (_Float16)(ws > 0.f ? acc / ws : 0.f);
-    if (d == 0) a.lse[row] = ws > 0.f ? m + fast_log2(ws) * kLn2 : -INFINITY;
-    (void)h;
-}
-
-template <int G>
-__global__ __launch_bounds__(NT) void decode_streamk_kernel(StreamKArgs a) {
-    __shared__ Smem<G> sm;
+// Hand-off of a split pair's partials between workgroups, possibly on different XCDs (whose L2
+// caches are not coherent with each other): contributors write their partial with agent-scope
+// atomic stores (write-through to the coherent level), wait until those stores have completed
+// (s_waitcnt), then count themselves in with an agent-scope atomic add; the last contributor reads
+// the partials with agent-scope atomic loads. No device-wide L2 write-back / invalidate
+// (which __threadfence() would issue in every contributing workgroup) is needed.
+template <class C>
+__global__ __launch_bounds__(C::NT) void decode_streamk_kernel(StreamKArgs a) {
+    constexpr int G = C::G, NW = C::NW, NT = C::NT;
+    __shared__ Smem<G, NW> sm;
+    __shared__ int pg[kRangeMax];
     __shared__ int s_last;
     const int w = blockIdx.x, tid = threadIdx.x;
 
     // Sequences without pages: the result is the merge of the extra partials alone (0 / -inf
     // when there are none).
-    for (int rr = w; rr < a.n_empty * a.Hq; rr += a.W) {
-        const size_t row = (size_t)a.empty_seq[rr / a.Hq] * a.Hq + rr % a.Hq;
-        for (int d = tid; d < kHeadDim; d += NT)
-            combine_row<G>(a, row, 0, d, false, 0.f, -INFINITY, nullptr, nullptr, 0);
-    }
+    for (int e = w; e < kargs()->n_empty * a.Hkv; e += a.W)
+        merge_sources<G, NW, false>(sm, kargs(), kargs()->empty_seq[e / a.Hkv], e % a.Hkv, false, 0, 0);
 
-    const int64_t u1 = a.U * (w + 1) / a.W;
-    int64_t u = a.U * w / a.W;
-    if (u >= u1) return;
-    int kvh = (int)(u / a.nnz);
-    int j = (int)(u - (int64_t)kvh * a.nnz);
-    int b = a.desc_b0[w];
-    while (true) {
-        const int pb = a.kv_indptr[b] - a.jbase, pe = a.kv_indptr[b + 1] - a.jbase;
-        const int len = (pe - pb - 1) * kPage + a.kv_last[b];
-        const int je = (int)min((int64_t)pe, (int64_t)j + (u1 - u));
-        const int t0 = (j - pb) * kPage;
-        const int t1 = min(len, (je - pb) * kPage);
-        process_range<G>(sm, a.q + ((size_t)b * a.Hq + kvh * G) * kHeadDim, a.k, a.v,
-                         a.kv_indices + a.jbase + pb, t0, t1, a.Hkv, kvh, a.scale_log2);
-        if (j == pb && je == pe) {
+    const int64_t u0 = a.U * w / a.W, u1 = a.U * (w + 1) / a.W;
+    const int R = (int)(u1 - u0);
+    if (R <= 0) return;
+    // page ids of this workgroup's range: units u0 .. u1-1 of the kv-head-major order are the
+    // consecutive page-table positions (u mod nnz), so they load before any descriptor arrives
+    for (int qq = tid; qq < R; qq += NT)
+        pg[qq] = a.kv_indices[a.jbase + (int)((u0 + qq) % a.nnz)];
+    const int nseg = kargs()->desc[(size_t)w * kDescInts];
+    __syncthreads();
+
+    for (int si = 0; si < nseg; ++si) {
+        const int32_t* sg = kargs()->desc + (size_t)w * kDescInts + 8 + kSegInts * si;
+        const int b = sg[0], kvh = sg[1], qa = sg[2], t0 = sg[4], t1 = sg[5];
+        process_range<C>(sm, a.q + ((size_t)b * a.Hq + kvh * G) * kHeadDim, a.k, a.v, pg + qa, t0,
+                         t0, t1, a.Hkv, kvh, a.scale_log2);
+        const int32_t* sg2 = kargs()->desc + (size_t)w * kDescInts + 8 + kSegInts * si;
+        const int w1 = sg2[6], nc = sg2[7];
+        if (nc == 1) {
             // the whole (sequence, kv head) pair was ours: final result
-            for (int idx = tid; idx < G * kHeadDim; idx += NT) {
-                const int h = idx / kHeadDim, d = idx % kHeadDim;
-                const size_t row = (size_t)b * a.Hq + kvh * G + h;
-                if (a.n_extra == 0) {
-                    a.out[row * kHeadDim + d] = (_Float16)sm.fo[h][d];
-                    if (d == 0) a.lse[row] = sm.flse[h];
-                } else {
-                    combine_row<G>(a, row, h, d, true, sm.fo[h][d], sm.flse[h], nullptr, nullptr, 0);
-                }
-            }
-        } else {
-            // one of several contributors: store the partial, count arrivals; the last merges
-            const int p = kvh * a.B + b;
-            const int64_t ufirst = (int64_t)kvh * a.nnz + pb, ulast = ufirst + (pe - pb) - 1;
-            const int w1 = (int)(((ufirst + 1) * a.W - 1) / a.U);
-            const int w2 = (int)(((ulast + 1) * a.W - 1) / a.U);
-            const size_t slot = (size_t)p + w;
-            for (int idx = tid; idx < G * kHeadDim; idx += NT) {
-                const int h = idx / kHeadDim, d = idx % kHeadDim;
-                a.part_o[(slot * G + h) * kHeadDim + d] = sm.fo[h][d];
-                if (d == 0) a.part_lse[slot * G + h] = sm.flse[h];
-            }
-            __threadfence();
-            __syncthreads();
-            if (tid == 0) {
-                const int old = atomicAdd(&a.counters[p], 1);
-                s_last = (old == w2 - w1) ? 1 : 0;
-            }
-            __syncthreads();
-            if (s_last) {
-                __threadfence();
-                const size_t s0 = (size_t)p + w1;
+            if (kargs()->n_extra == 0) {
                 for (int idx = tid; idx < G * kHeadDim; idx += NT) {
                     const int h = idx / kHeadDim, d = idx % kHeadDim;
                     const size_t row = (size_t)b * a.Hq + kvh * G + h;
-                    combine_row<G>(a, row, h, d, false, 0.f, -INFINITY,
-                                   a.part_o + (s0 * G + h) * kHeadDim + d, a.part_lse + s0 * G + h,
-                                   w2 - w1 + 1);
+                    kargs()->out[row * kHeadDim + d] = (_Float16)sm.fo[h][d];
+                    if (d == 0) kargs()->lse[row] = sm.flse[h];
                 }
-                if (tid == 0) atomicExch(&a.counters[p], 0);
+            } else {
+                merge_sources<G, NW, false>(sm, kargs(), b, kvh, true, 0, 0);
             }
-        }
-        u += je - j;
-        j = je;
-        if (u >= u1) break;
-        if (j == a.nnz) {
-            ++kvh;
-            j = 0;
-            b = a.b_first;
         } else {
-            ++b;
-            while (a.kv_indptr[b + 1] == a.kv_indptr[b]) ++b;
+            // one of nc contributors: store the partial with agent-scope atomic stores, count
+            // arrivals; the last one merges all nc partials in workgroup order
+            const int p = kvh * a.B + b;
+            const size_t slot = (size_t)p + w;
+            for (int idx = tid; idx < G * kHeadDim; idx += NT) {
+                const int h = idx / kHeadDim, d = idx % kHeadDim;
+                __hip_atomic_store(kargs()->part_o + (slot * G + h) * kHeadDim + d, sm.fo[h][d],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (d == 0)
+                    __hip_atomic_store(kargs()->part_lse + slot * G + h, sm.flse[h], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __builtin_amdgcn_s_waitcnt(0);   // this thread's partial stores have completed
+            __syncthreads();
+            if (tid == 0) {
+                const int old = __hip_atomic_fetch_add(&kargs()->counters[p], 1, __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
+                s_last = (old == nc - 1) ? 1 : 0;
+            }
+            __syncthreads();
+            if (s_last) {
+                merge_sources<G, NW, true>(sm, kargs(), b, kvh, false, (int64_t)p + w1, nc);
+                if (tid == 0)
+                    __hip_atomic_store(&kargs()->counters[p], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
         __syncthreads();  // sm is reused by the next segment
     }
@@ -476,46 +617,93 @@ __global__ void fill_i32_kernel(int32_t* p, int32_t value, size_t n) {
         p[i] = value;
 }
 
-template <int G>
-const void* partial_kernel_ptr() { return reinterpret_cast<const void*>(&decode_partial_kernel<G>); }
-template <int G>
-const void* streamk_kernel_ptr() { return reinterpret_cast<const void*>(&decode_streamk_kernel<G>); }
-
 int occupancy_of(const void* fn, int threads) {
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, 0) != hipSuccess) return 1;
     return n > 0 ? n : 1;
 }
 
+// Kernel shapes: the default per G, plus G = 4 alternatives selected by PDATTN_VARIANT while
+// tuning.
+template <int G>
+using DefaultCfg = Cfg<G, (G >= 8 ? 16 : 8), 8, 2>;
+using V1 = Cfg<4, 8, 8, 3>;
+using V2 = Cfg<4, 16, 8, 3>;
+using V3 = Cfg<4, 16, 8, 4>;
+using V4 = Cfg<4, 16, 4, 4>;
+using V5 = Cfg<4, 8, 4, 3>;
+using V6 = Cfg<4, 16, 4, 6>;
+
+int variant_env() {
+    const char* v = getenv("PDATTN_VARIANT");
+    return v ? atoi(v) : 0;
+}
+
+template <class C>
+void launch_p(const PartialArgs& a, hipStream_t s) {
+    decode_partial_kernel<C><<<dim3(a.num_chunks, a.B * a.Hkv), C::NT, 0, s>>>(a);
+}
+template <class C>
+void launch_s(const StreamKArgs& a, hipStream_t s) {
+    decode_streamk_kernel<C><<<a.W, C::NT, 0, s>>>(a);
+}
+template <class C>
+int occ_p() { return occupancy_of(reinterpret_cast<const void*>(&decode_partial_kernel<C>), C::NT); }
+template <class C>
+int occ_s() { return occupancy_of(reinterpret_cast<const void*>(&decode_streamk_kernel<C>), C::NT); }
+
+#define PD_DISPATCH(G, FN, ...)                                  \
+    do {                                                         \
+        if ((G) == 4) {                                          \
+            switch (variant_env()) {                             \
+                case 1: FN<V1>(__VA_ARGS__); break;              \
+                case 2: FN<V2>(__VA_ARGS__); break;              \
+                case 3: FN<V3>(__VA_ARGS__); break;              \
+                case 4: FN<V4>(__VA_ARGS__); break;              \
+                case 5: FN<V5>(__VA_ARGS__); break;              \
+                case 6: FN<V6>(__VA_ARGS__); break;              \
+                default: FN<DefaultCfg<4>>(__VA_ARGS__); break;  \
+            }                                                    \
+        } else if ((G) == 1) FN<DefaultCfg<1>>(__VA_ARGS__);     \
+        else if ((G) == 2) FN<DefaultCfg<2>>(__VA_ARGS__);       \
+        else FN<DefaultCfg<8>>(__VA_ARGS__);                     \
+    } while (0)
+
+#define PD_DISPATCH_RET(G, FN)                                   \
+    do {                                                         \
+        if ((G) == 4) {                                          \
+            switch (variant_env()) {                             \
+                case 1: return FN<V1>();                         \
+                case 2: return FN<V2>();                         \
+                case 3: return FN<V3>();                         \
+                case 4: return FN<V4>();                         \
+                case 5: return FN<V5>();                         \
+                case 6: return FN<V6>();                         \
+                default: return FN<DefaultCfg<4>>();             \
+            }                                                    \
+        } else if ((G) == 1) return FN<DefaultCfg<1>>();         \
+        else if ((G) == 2) return FN<DefaultCfg<2>>();           \
+        return FN<DefaultCfg<8>>();                              \
+    } while (0)
+
 }  // namespace
 
 hipError_t launch_decode_partial(const PartialArgs& a, int G, hipStream_t s) {
-    dim3 grid(a.num_chunks, a.B * a.Hkv);
-    switch (G) {
-        case 1: decode_partial_kernel<1><<<grid, NT, 0, s>>>(a); break;
-        case 2: decode_partial_kernel<2><<<grid, NT, 0, s>>>(a); break;
-        case 4: decode_partial_kernel<4><<<grid, NT, 0, s>>>(a); break;
-        case 8: decode_partial_kernel<8><<<grid, NT, 0, s>>>(a); break;
-        default: return hipErrorInvalidValue;
-    }
+    if (G != 1 && G != 2 && G != 4 && G != 8) return hipErrorInvalidValue;
+    PD_DISPATCH(G, launch_p, a, s);
     return hipGetLastError();
 }
 
 hipError_t launch_merge_states(const float* part_o, const float* part_lse, _Float16* out,
                                float* lse, int rows, int num_chunks, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    merge_states_kernel<<<rows, kHeadDim, 0, s>>>(part_o, part_lse, out, lse, num_chunks);
+    merge_states_kernel<<<rows, kMergeThreads, 0, s>>>(part_o, part_lse, out, lse, num_chunks);
     return hipGetLastError();
 }
 
 hipError_t launch_decode_streamk(const StreamKArgs& a, int G, hipStream_t s) {
-    switch (G) {
-        case 1: decode_streamk_kernel<1><<<a.W, NT, 0, s>>>(a); break;
-        case 2: decode_streamk_kernel<2><<<a.W, NT, 0, s>>>(a); break;
-        case 4: decode_streamk_kernel<4><<<a.W, NT, 0, s>>>(a); break;
-        case 8: decode_streamk_kernel<8><<<a.W, NT, 0, s>>>(a); break;
-        default: return hipErrorInvalidValue;
-    }
+    if (G != 1 && G != 2 && G != 4 && G != 8) return hipErrorInvalidValue;
+    PD_DISPATCH(G, launch_s, a, s);
     return hipGetLastError();
 }
 
@@ -526,22 +714,7 @@ hipError_t launch_fill_i32(int32_t* p, int32_t value, size_t n, hipStream_t s) {
     return hipGetLastError();
 }
 
-int occupancy_decode_partial(int G) {
-    switch (G) {
-        case 1: return occupancy_of(partial_kernel_ptr<1>(), NT);
-        case 2: return occupancy_of(partial_kernel_ptr<2>(), NT);
-        case 4: return occupancy_of(partial_kernel_ptr<4>(), NT);
-        default: return occupancy_of(partial_kernel_ptr<8>(), NT);
-    }
-}
-
-int occupancy_decode_streamk(int G) {
-    switch (G) {
-        case 1: return occupancy_of(streamk_kernel_ptr<1>(), NT);
-        case 2: return occupancy_of(streamk_kernel_ptr<2>(), NT);
-        case 4: return occupancy_of(streamk_kernel_ptr<4>(), NT);
-        default: return occupancy_of(streamk_kernel_ptr<8>(), NT);
-    }
-}
+int occupancy_decode_partial(int G) { PD_DISPATCH_RET(G, occ_p); }
+int occupancy_decode_streamk(int G) { PD_DISPATCH_RET(G, occ_s); }
 
 }  // namespace pdattn

@@ -6,34 +6,42 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// Streams the buffer once with 16-byte loads (four in flight per thread per iteration) and
-// folds it into one word; the store happens only on a sentinel match, so the loads stay live.
-// Same measurement as stream_read (qilem/cuda-kernel-lab, 01_decode_attention.cu:257-265).
+// Streams the buffer once with 16-byte non-temporal loads (eight in flight per thread per
+// iteration) and folds it into one word; the store happens only on a sentinel match, so the loads
+// stay live. Same measurement as stream_read (qilem/cuda-kernel-lab, 01_decode_attention.cu:257-265);
+// the load width, depth and hint are the ones that measured fastest on MI355X.
 __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restrict__ p, size_t n,
                                                            uint32_t* sink) {
+    constexpr int U = 8;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
     uint32_t acc = 0;
-    for (; i + 3 * stride < n; i += 4 * stride) {
-        const u32x4 a = p[i], b = p[i + stride], c = p[i + 2 * stride], d = p[i + 3 * stride];
-        acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+    for (; i + (U - 1) * stride < n; i += U * stride) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(p + i + u * stride);
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
     }
     for (; i < n; i += stride) {
-        const u32x4 a = p[i];
+        const u32x4 a = __builtin_nontemporal_load(p + i);
         acc ^= a.x ^ a.y ^ a.z ^ a.w;
     }
     if (acc == 0x9e3779b9u) sink[0] = acc;
 }
 
-// Read-modify-write of every 16-byte word, so that the caches (L2 per XCD and the Infinity
-// Cache) end up holding this buffer instead of what is timed next.
+// Reads every 16-byte word once (no writes), so that the caches (L2 per XCD and the Infinity
+// Cache) end up holding this buffer instead of what is timed next. A read-only sweep leaves no
+// dirty lines behind; a write sweep would leave up to the whole Infinity Cache dirty, and the
+// timed kernel would pay for writing it back.
 __global__ __launch_bounds__(256) void flush_kernel(u32x4* __restrict__ p, size_t n) {
     const size_t stride = (size_t)gridDim.x * blockDim.x;
+    uint32_t acc = 0;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
-        u32x4 a = p[i];
-        a.x += 1u;
-        p[i] = a;
+        const u32x4 a = p[i];
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
     }
+    if (acc == 0x9e3779b9u) p[0].x = acc;   // keeps the loads live; never taken in practice
 }
 
 }  // namespace

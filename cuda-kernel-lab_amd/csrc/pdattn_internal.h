@@ -10,8 +10,6 @@ namespace pdattn {
 
 constexpr int kHeadDim = 128;
 constexpr int kPage = 16;
-constexpr int kDecodeWaves = 4;               // waves per decode workgroup
-constexpr int kDecodeThreads = kDecodeWaves * 64;
 
 // Arguments of the uniform-chunk partial kernel (the reference's decode_partial launch).
 struct PartialArgs {
@@ -27,28 +25,36 @@ struct PartialArgs {
     float scale_log2;         // sm_scale * log2(e)
 };
 
-// Arguments of the balanced single-launch kernel.
+// Balanced single-launch kernel: per-workgroup descriptor written by the host planner.
+// desc[w * kDescInts + 0] = number of segments; segment s at desc[w * kDescInts + 8 + 8 s] =
+//   {b, kvh, qa, npg, t0, t1, w1, nc}: sequence b, kv head kvh, pages [qa, qa + npg) of the
+//   workgroup's page range, tokens [t0, t1) of the sequence (t0 is the first token of page qa),
+//   first contributing workgroup w1 and contributor count nc of the (b, kvh) pair (nc = 1: this
+//   workgroup covers the whole pair).
+constexpr int kSegMax = 8;                 // segments per workgroup
+constexpr int kSegInts = 8;
+constexpr int kDescInts = 8 + kSegMax * kSegInts;
+constexpr int kRangeMax = 2048;            // pages per workgroup (page ids staged in LDS)
+
 struct StreamKArgs {
     const _Float16* q;
     const uint8_t*  k;
     const uint8_t*  v;
-    const int32_t*  kv_indptr;
     const int32_t*  kv_indices;
-    const int32_t*  kv_last;
     _Float16*       out;
     float*          lse;
-    const int32_t*  desc_b0;      // [W] first sequence of each workgroup's page range
+    const int32_t*  desc;         // [W * kDescInts]
     const int32_t*  empty_seq;    // [n_empty] sequences with no pages
     int32_t*        counters;     // [B*Hkv] arrival counters of split pairs (zero between launches)
     float*          part_o;       // [(B*Hkv + W) * G * 128] partial slots, slot = pair + workgroup
     float*          part_lse;     // [(B*Hkv + W) * G]
-    // extra partials merged into every row (cascade prefix): [B*Hq, extra_stride] slots
+    // extra partials merged into every row (cascade prefix): [B*Hq, n_extra] slots
     const float*    extra_o;
     const float*    extra_lse;
-    int64_t U;                    // Hkv * nnz page units
+    int64_t U;                    // Hkv * nnz page units, kv-head-major
     int nnz, jbase;               // pages in the table, kv_indptr[0]
-    int B, Hq, Hkv, W, n_empty, b_first;
-    int n_extra, extra_stride;
+    int B, Hq, Hkv, W, n_empty;
+    int n_extra;
     float scale_log2;
 };
 

@@ -211,9 +211,10 @@ void pdattn_cascade_plan_destroy(pdattn_cascade_plan* plan);
  * to *sink only on a sentinel match (stream_read, 01_decode_attention.cu:257-265). */
 int pdattn_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream);
 
-/* Reads and rewrites `bytes` (a multiple of 16) of `buf` so that caches hold none of the data
- * timed next; size it above the 256 MB Infinity Cache. No counterpart in the reference, which
- * flushes with cudaMemsetAsync (common/bench.cuh:120, 159). */
+/* Reads `bytes` (a multiple of 16) of `buf` once so that the caches hold none of the data timed
+ * next; size it above the 256 MB Infinity Cache. Read-only, so it leaves no dirty lines whose
+ * write-back the timed kernel would pay for. Replaces the reference's cudaMemsetAsync flush
+ * (common/bench.cuh:120, 159). */
 int pdattn_flush_cache(void* buf, size_t bytes, void* stream);
 
 typedef struct pdattn_device_info {
