@@ -32,7 +32,7 @@
 /* ---- fault injection (test-only) ------------------------------------------------------- */
 enum {
     FAULT_NONE = 0,
-    FAULT_PAGE_OFF_BY_ONE = 1,  /* reads the next entry of kv_indices                        */
+    FAULT_PAGE_OFF_BY_ONE = 1,  /* reads the next page of the sequence (wrapping)             */
     FAULT_KVH_MODULO = 2,       /* maps q head h to kv head h % Hkv instead of h / G          */
     FAULT_NO_SCALE = 3,         /* drops sm_scale                                             */
     FAULT_FULL_LAST_PAGE = 4,   /* ignores kv_last_page_len (treats the last page as full)    */
@@ -97,7 +97,7 @@ static int seq_len(const int32_t* indptr, const int32_t* last, int b) {
 /* Element offset of row (key) `key` of sequence b, kv head kvh. Follows 01:111-112 / 01:383-384. */
 static size_t kv_offset(const int32_t* indptr, const int32_t* indices, int Hkv, int b, int key, int kvh) {
     int pos = indptr[b] + key / PAGE;
-    if (g_fault == FAULT_PAGE_OFF_BY_ONE) pos += 1;
+    if (g_fault == FAULT_PAGE_OFF_BY_ONE) pos = indptr[b] + (key / PAGE + 1) % (indptr[b + 1] - indptr[b]);
     int page = indices[pos];
     if (g_fault == FAULT_SLOT_TRANSPOSE)
         return (((size_t)page * Hkv + kvh) * PAGE + key % PAGE) * HEAD_DIM;

@@ -1,0 +1,49 @@
+"""Static checks of the gfx950 code objects -- CPU only (hipcc cross-compiles).
+
+* No kernel makes a device-function call: the balanced kernel reads its arguments through the
+  kernarg-segment pointer, which is only valid in the kernel body (in a called function it is
+  null), and calls would also cost registers and latency in the hot loop.
+* No packed-FP32 instructions are emitted (the build disables them).
+* No kernel spills registers to scratch (except the G = 8 instance of the balanced kernel, which
+  is allowed a small spill).
+"""
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CSRC = os.path.join(ROOT, "cuda-kernel-lab_amd", "csrc")
+HIPCC = "/opt/rocm/bin/hipcc"
+FLAGS = ["-O3", "-std=c++17", "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang",
+         "-packed-fp32-ops", "--cuda-device-only"]
+
+
+def _asm(name, tmp_path):
+    out = tmp_path / (name + ".s")
+    subprocess.run([HIPCC, *FLAGS, "-S", os.path.join(CSRC, name + ".hip"), "-o", str(out)],
+                   check=True, stderr=subprocess.DEVNULL)
+    return out.read_text()
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
+@pytest.mark.parametrize("name", ["decode", "cascade", "misc"])
+def test_no_calls_no_packed_fp32(name, tmp_path):
+    asm = _asm(name, tmp_path)
+    assert "s_swappc_b64" not in asm, f"{name}.hip: a kernel calls a device function"
+    assert not re.search(r"\bv_pk_(add|mul|fma)_f32\b", asm), f"{name}.hip: packed FP32 emitted"
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
+def test_no_scratch_spills(tmp_path):
+    out = subprocess.run([HIPCC, *FLAGS, "-c", os.path.join(CSRC, "decode.hip"), "-o", str(tmp_path / "d.o"),
+                          "-Rpass-analysis=kernel-resource-usage"], capture_output=True, text=True)
+    text = out.stderr
+    names = re.findall(r"Function Name: (\S+)", text)
+    spills = re.findall(r"VGPRs Spill: (\d+)", text)
+    assert names and len(names) == len(spills)
+    for n, sp in zip(names, spills):
+        if "streamk" in n and "Li8E" in n.split("Cfg")[1][:6]:
+            continue
+        assert int(sp) == 0, f"{n} spills {sp} VGPRs"

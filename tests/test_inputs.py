@@ -1,0 +1,40 @@
+"""Synthetic batch builders (restating Batch / make_shared_prefix_batch,
+01_decode_attention.cu:333-368, 714-742) -- CPU only."""
+import numpy as np
+
+from pdattn import inputs
+
+
+def test_batch_page_table():
+    bt = inputs.make_batch([1, 16, 17, 0, 4097], 8, 2, seed=5)
+    assert list(bt.indptr) == [0, 1, 2, 4, 4, 261]
+    assert list(bt.last) == [1, 16, 1, 0, 1]
+    assert sorted(bt.indices) == list(range(bt.num_pages))       # a permutation of the pages
+    assert bt.k.shape == (261, 16, 2, 128) and bt.q.shape == (5, 8, 128)
+    again = inputs.make_batch([1, 16, 17, 0, 4097], 8, 2, seed=5)
+    assert np.array_equal(bt.indices, again.indices) and np.array_equal(bt.k, again.k)
+
+
+def test_shared_prefix_batch():
+    bt = inputs.make_shared_prefix_batch(64, [1, 17, 40], 8, 8, seed=13)
+    pp = 4
+    first = bt.indices[:pp]
+    for b in range(bt.B):
+        assert np.array_equal(bt.indices[bt.indptr[b]:bt.indptr[b] + pp], first)
+    private = np.concatenate([bt.indices[bt.indptr[b] + pp:bt.indptr[b + 1]] for b in range(bt.B)])
+    assert len(set(private)) == len(private) and not set(private) & set(first)
+    assert bt.num_pages == pp + len(private)
+    assert bt.lens == [65, 81, 104]
+
+
+def test_algorithmic_bytes_formula():
+    bt = inputs.make_batch([32768], 32, 8, seed=11, fill=False)
+    assert bt.algorithmic_bytes() == 134_242_444           # the figure quoted for 1 x 32K
+    bt = inputs.make_batch([1024] * 64, 32, 8, seed=11, fill=False)
+    assert bt.algorithmic_bytes() == 269_509_124
+
+
+def test_ragged_lengths_are_seeded():
+    a = inputs.ragged_lens(64, 256, 4096, 11)
+    assert a == inputs.ragged_lens(64, 256, 4096, 11)
+    assert min(a) >= 256 and max(a) <= 4096
