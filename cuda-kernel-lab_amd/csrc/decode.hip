@@ -75,12 +75,56 @@ __device__ __forceinline__ float row_sum(float v) {
     return v;
 }
 
+// Combine of the 64/LPR row groups of a wave (lanes LPR apart hold the same head dims), leaving
+// the result in every lane: row_ror:8 pairs the two groups of a 16-lane row (LPR = 8), then
+// v_permlane16_swap / v_permlane32_swap pair whole 16-lane rows, all in the VALU. After
+// swap(a, b) the two results hold, in every lane, the values of both rows of its pair (rows
+// r and r^1 for the 16-lane swap, r and r^2 for the 32-lane swap), always in the same order, so
+// r0 + r1 is bitwise the same in all lanes. The second operand is passed through an empty asm
+// statement: given the same SSA value twice, the compiler treats the two results as equal and
+// drops the second one.
+__device__ __forceinline__ unsigned opaque_copy(unsigned v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+template <bool ROWS32>
+__device__ __forceinline__ void row_pair(float v, float& a, float& b) {
+    const unsigned x = __builtin_bit_cast(unsigned, v);
+    unsigned r0, r1;
+    if constexpr (ROWS32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(x, opaque_copy(x), false, false);
+        r0 = r[0]; r1 = r[1];
+    } else {
+        const auto r = __builtin_amdgcn_permlane16_swap(x, opaque_copy(x), false, false);
+        r0 = r[0]; r1 = r[1];
+    }
+    a = __builtin_bit_cast(float, r0);
+    b = __builtin_bit_cast(float, r1);
+}
+
 // Reinterprets one 32-bit word as two fp16. The word is taken by value: bit-casting an
 // ext-vector element expression in place was observed to read element 0 for every index.
 __device__ __forceinline__ f16x2 as_h2(uint32_t w) { return __builtin_bit_cast(f16x2, w); }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+template <int LPR>
+__device__ __forceinline__ float xgroup_sum(float v) {
+    float a, b;
+    if constexpr (LPR == 8) v += dpp<0x128>(v);   // row_ror:8
+    row_pair<false>(v, a, b);
+    row_pair<true>(a + b, a, b);
+    return a + b;
+}
+template <int LPR>
+__device__ __forceinline__ float xgroup_max(float v) {
+    float a, b;
+    if constexpr (LPR == 8) v = fmaxf(v, dpp<0x128>(v));
+    row_pair<false>(v, a, b);
+    row_pair<true>(fmaxf(a, b), a, b);
+    return fmaxf(a, b);
+}
 
 template <class C>
 struct WaveState {
@@ -263,22 +307,12 @@ __device__ __forceinline__ void process_range(Smem<C::G, C::NW>& sm, const _Floa
     // merge the 64/LPR row-group states of this wave (lanes LPR apart hold the same dims)
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        float M = st.m[h];
-#pragma unroll
-        for (int off = g::LPR; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
+        const float M = xgroup_max<g::LPR>(st.m[h]);
         const float a = (st.m[h] == -INFINITY) ? 0.f : fast_exp2(st.m[h] - M);
-        float l = st.l[h] * a;
+        st.l[h] = xgroup_sum<g::LPR>(st.l[h] * a);
 #pragma unroll
-        for (int off = g::LPR; off < 64; off <<= 1) l += __shfl_xor(l, off);
-#pragma unroll
-        for (int d = 0; d < g::DPL; ++d) {
-            float v = st.o[h][d] * a;
-#pragma unroll
-            for (int off = g::LPR; off < 64; off <<= 1) v += __shfl_xor(v, off);
-            st.o[h][d] = v;
-        }
+        for (int d = 0; d < g::DPL; ++d) st.o[h][d] = xgroup_sum<g::LPR>(st.o[h][d] * a);
         st.m[h] = M;
-        st.l[h] = l;
     }
     if (lane < g::LPR) {
 #pragma unroll
@@ -360,9 +394,12 @@ __device__ __forceinline__ void lse_accumulate(float& m, float& ws, float4& acc,
 // One pass: each thread owns one 4-dim quad of one row and every TPQ-th source, issues all its
 // loads, accumulates them online, and the TPQ partial states of a quad are combined in order
 // through LDS. Writes fp16 out and fp32 lse; a row whose every source is empty gets 0 / -inf.
-template <int G, int NW, bool ATOMIC_LOADS>
+template <int G, int NW, bool ACQUIRE>
 __device__ __forceinline__ void merge_sources(Smem<G, NW>& sm, KArgPtr a, int b, int kvh, bool own,
                                               int64_t s0, int nslots) {
+    // partials written by other workgroups (write-through atomic stores, completed before their
+    // arrival was counted): drop any stale copies this XCD's caches hold, then plain loads
+    if constexpr (ACQUIRE) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     constexpr int NT = NW * 64;
     constexpr int Q = G * 32;          // 4-dim quads of the G rows
     constexpr int TPQ = NT / Q;        // threads per quad
@@ -386,16 +423,8 @@ __device__ __forceinline__ void merge_sources(Smem<G, NW>& sm, KArgPtr a, int b,
         if (k < nslots) {
             const float* pl = a->part_lse + (s0 + k) * G + h;
             const float* po = a->part_o + ((s0 + k) * G + h) * kHeadDim + d0;
-            if constexpr (ATOMIC_LOADS) {
-                l = __hip_atomic_load(pl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                o = make_float4(__hip_atomic_load(po, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                                __hip_atomic_load(po + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                                __hip_atomic_load(po + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                                __hip_atomic_load(po + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-            } else {
-                l = *pl;
-                o = *reinterpret_cast<const float4*>(po);
-            }
+            l = *pl;
+            o = *reinterpret_cast<const float4*>(po);
             return;
         }
         const size_t e = (row0 + h) * n_extra + (k - nslots);
@@ -536,9 +565,10 @@ __global__ __launch_bounds__(kMergeThreads) void merge_states_kernel(const float
 // Hand-off of a split pair's partials between workgroups, possibly on different XCDs (whose L2
 // caches are not coherent with each other): contributors write their partial with agent-scope
 // atomic stores (write-through to the coherent level), wait until those stores have completed
-// (s_waitcnt), then count themselves in with an agent-scope atomic add; the last contributor reads
-// the partials with agent-scope atomic loads. No device-wide L2 write-back / invalidate
-// (which __threadfence() would issue in every contributing workgroup) is needed.
+// (s_waitcnt), then count themselves in with an agent-scope atomic add; the last contributor
+// invalidates its own caches once (agent-scope acquire) and reads the partials with plain
+// vector loads. No L2 write-back (which __threadfence() would issue in every contributing
+// workgroup, flushing and invalidating that XCD's whole L2) is needed.
 template <class C>
 __global__ __launch_bounds__(C::NT) void decode_streamk_kernel(StreamKArgs a) {
     constexpr int G = C::G, NW = C::NW, NT = C::NT;
