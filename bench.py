@@ -2,9 +2,16 @@
 
 A "step" is one decode-attention launch over one batch already resident in HBM: the balanced
 single-launch path (pdattn_plan_run), H_q=32, H_kv=8, d=128, page 16, fp16 q/K/V ~ N(0,1) with
-shuffled pages (seeded). Before every step a 1 GiB buffer (4x the 256 MB Infinity Cache) is read
-and rewritten so the step starts cold; each step is bracketed by HIP events on the stream the
-kernel runs on, and ms_per_step is the median over the timed steps.
+shuffled pages (seeded).
+
+Two timings, both cold-cache:
+  * value / ms_per_step -- the reference's method (common/bench.cuh:144-175): before every step a
+    1 GiB buffer (4x the 256 MB Infinity Cache) is read by a flush kernel, each step is bracketed
+    by HIP events on the stream the kernel runs on, methods are interleaved, and the median is
+    reported. The event pair includes the dispatch of the kernel after the first event.
+  * roofline.achieved -- the kernel's average launch duration: K launches back to back between one
+    event pair, each over its own copy of K/V (copies totalling >= 1 GiB, so every launch reads
+    lines that have left the caches). This is what a trace of the kernel reports as its duration.
 
 Headline workload: B=1, L=32768; `value` is its achieved HBM GB/s
 (algorithmic bytes / median step time). The same line carries the 64 x 1K workload the metric also
@@ -32,7 +39,10 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", default="", help="run only one workload: 32k | 64x1k | cascade")
+    ap.add_argument("--only", default="", choices=["", "32k", "64x1k", "cascade"],
+                    help="run one workload only (for profiling)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only torch copies of COPY_BYTES (known-size traffic for counter runs)")
     return ap.parse_args()
 
 
@@ -126,6 +136,11 @@ def uniform_runner(bt, t, stream):
     return fn, (p, ws), nc
 
 
+ROT_BYTES = 1 << 30
+COPY_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_streamk_1x32k_traffic.md")
+
+
 def ceiling_gbs(timer, steps):
     """Achievable streaming-read bandwidth: 2 GiB of 16-byte loads (stream_read)."""
     import torch
@@ -137,6 +152,61 @@ def ceiling_gbs(timer, steps):
     ms = timer.run([fn], max(5, steps // 3), 2)[0]
     del buf
     return nbytes / (statistics.median(ms) * 1e-3) / 1e9
+
+
+def rotated_kernel_us(plan, ws, t, stream, steps):
+    """Average duration of one balanced launch, K launches back to back between one event pair.
+
+    Launch i reads K/V copy i mod n; the n copies total >= ROT_BYTES (4x the Infinity Cache), so
+    each launch reads lines no cache still holds, with no flush kernel between launches."""
+    import torch
+    kv_bytes = 2 * t["k"].numel() * t["k"].element_size()
+    n = max(2, -(-ROT_BYTES // kv_bytes))
+    ks, vs = [t["k"]], [t["v"]]
+    for _ in range(n - 1):
+        ks.append(torch.empty_like(t["k"]).normal_())
+        vs.append(torch.empty_like(t["v"]).normal_())
+
+    def launch(i):
+        plan.run(t["q"], ks[i % n], vs[i % n], t["indptr"], t["indices"], t["last"], t["out"],
+                 t["lse"], ws, ws.numel(), stream=stream)
+    for i in range(n):
+        launch(i)
+    k = max(steps, 4 * n)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(k):
+        launch(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    del ks, vs
+    return e0.elapsed_time(e1) * 1e3 / k, k, n
+
+
+def measured_traffic():
+    """HBM bytes per launch of the headline kernel from the committed counter summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by its copy-kernel calibration), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
+
+
+def copy_calibration(steps):
+    """Known-size traffic for counter calibration: dst.copy_(src) of COPY_BYTES, steps times."""
+    import torch
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.int32, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": COPY_BYTES, "launches": steps}))
 
 
 def cpu_baseline(bt_lens, Hq, Hkv, seed, budget_s=10.0):
@@ -160,87 +230,122 @@ def cpu_baseline(bt_lens, Hq, Hkv, seed, budget_s=10.0):
                       f"x{runs} runs, {per * 1e3:.1f} ms/run on {threads} threads"}
 
 
+def decode_workload(timer, lens, args, with_uniform):
+    """Median cold step (flush before each), kernel duration (rotated back-to-back), plan info."""
+    import torch
+    s = timer.stream
+    bt, t = make_device_batch(lens, 32, 8, seed=11)
+    fn_sk, plan, ws = streamk_runner(bt, t, s)
+    fns = [fn_sk]
+    if with_uniform:
+        fn_un, keep_un, nc = uniform_runner(bt, t, s)
+        fns.append(fn_un)
+    times = timer.run(fns, args.steps, args.warmup, rounds=3)
+    nbytes = bt.algorithmic_bytes()
+    ms = statistics.median(times[0])
+    kern_us, k, ncopy = rotated_kernel_us(plan, ws, t, s, args.steps)
+    info = plan.info()
+    r = {"bytes": nbytes, "ms": ms, "steps": len(times[0]), "kernel_us": kern_us,
+         "kernel_launches": k, "kv_copies": ncopy, "workgroups": info.workgroups}
+    if with_uniform:
+        mu = statistics.median(times[1])
+        r["uniform"] = {"us_per_step": round(mu * 1e3, 2), "chunks": nc,
+                        "GB/s": round(nbytes / (mu * 1e-3) / 1e9, 1)}
+        del keep_un
+    del t, ws
+    torch.cuda.empty_cache()
+    return r
+
+
+def gbs(nbytes, seconds):
+    return nbytes / seconds / 1e9
+
+
+def cascade_workload(timer, args):
+    """64 requests x (8192 shared + 512 private): cascade vs the non-shared kernel, same method."""
+    import pdattn
+    s = timer.stream
+    bt3, t3 = make_device_batch(None, 32, 8, seed=21, shared_prefix=8192, suffix=[512] * 64)
+    f3n, plan3, ws3 = streamk_runner(bt3, t3, s)
+    base = pdattn.make_params(t3["q"], t3["k"], t3["v"], t3["indptr"], t3["indices"], t3["last"],
+                              bt3.B, 32, 8)
+    cp = pdattn.CascadePlan(base, bt3.indptr, bt3.indices, bt3.lens, t3["indices"])
+    cws = pdattn.Workspace()
+    cp.decode(t3["out"], t3["lse"], cws, s)  # uploads the schedule
+    f3c = lambda: cp.decode(t3["out"], t3["lse"], cws, s)  # noqa: E731
+    w3n, w3c = timer.run([f3n, f3c], args.steps, args.warmup, rounds=3)
+    mn, mc = statistics.median(w3n), statistics.median(w3c)
+    ci = cp.info()
+    out = {"non_shared_us": round(mn * 1e3, 2), "cascade_us": round(mc * 1e3, 2),
+           "speedup": round(mn / mc, 2), "prefix_chunks": ci.prefix_chunks,
+           "prefix_workgroups": ci.prefix_workgroups, "suffix_workgroups": ci.suffix_workgroups}
+    cp.close()
+    pdattn.workspace_release(cws)
+    del t3, ws3
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              f"(the path shards by sequence / kv head with no exchange; see DESIGN.md)",
+              f"(one GPU per box; the path would shard by sequence / kv head with no exchange)",
               file=sys.stderr)
         sys.exit(2)
     import torch
     import pdattn
     pdattn.lib()
+    if args.copy_calibration:
+        copy_calibration(args.steps)
+        return
     dinfo = pdattn.device_info()
     timer = Timer()
-    s = timer.stream
-    result = {}
-
-    # headline: B=1, L=32768
-    bt, t = make_device_batch([32768], 32, 8, seed=11)
-    fn_sk, plan, ws = streamk_runner(bt, t, s)
-    fn_un, keep_un, nc = uniform_runner(bt, t, s)
-    w_sk, w_un = timer.run([fn_sk, fn_un], args.steps, args.warmup, rounds=3)
-    ms_sk, ms_un = statistics.median(w_sk), statistics.median(w_un)
-    mean_sk = statistics.mean(w_sk)
-    bytes32 = bt.algorithmic_bytes()
-    info = plan.info()
-    gbs = bytes32 / (ms_sk * 1e-3) / 1e9
-    result.update(
-        metric=METRIC, value=round(gbs, 1), unit="GB/s", n_gpus=1, steps=len(w_sk),
-        warmup=args.warmup, ms_per_step=round(ms_sk, 5), us_per_step=round(ms_sk * 1e3, 2),
-        pct_of_peak=round(100 * gbs / PEAK_GBS, 1), higher_is_better=True, scaling="weak",
-        vs_baseline=None, dtype="fp16 in, fp32 accumulate", data="synthetic N(0,1), seeded",
-        config={"workload": "paged GQA decode B=1 L=32768 (configs[1])", "B": 1, "L": 32768,
-                "Hq": 32, "Hkv": 8, "head_dim": 128, "page": 16, "seed": 11,
-                "path": "pdattn_plan_run (balanced single launch)", "workgroups": info.workgroups,
-                "algorithmic_bytes": bytes32, "cache_flush_bytes": FLUSH_BYTES},
-        roofline={"bound": "hbm", "achieved": round(bytes32 / (mean_sk * 1e-3) / 1e9, 1),
-                  "peak": PEAK_GBS, "unit": "GB/s",
-                  "frac": round(bytes32 / (mean_sk * 1e-3) / 1e9 / PEAK_GBS, 4), "traffic": None},
-        uniform_path={"us_per_step": round(ms_un * 1e3, 2), "chunks": nc,
-                      "GB/s": round(bytes32 / (ms_un * 1e-3) / 1e9, 1)},
+    if args.only == "cascade":
+        print(json.dumps({"cascade_64x(8192+512)": cascade_workload(timer, args)}))
+        return
+    lens = [1024] * 64 if args.only == "64x1k" else [32768]
+    name = ("paged GQA decode B=64 L=1024 (metric's 64x1K)" if args.only == "64x1k"
+            else "paged GQA decode B=1 L=32768 (configs[1])")
+    h = decode_workload(timer, lens, args, with_uniform=not args.only)
+    value = gbs(h["bytes"], h["ms"] * 1e-3)
+    achieved = gbs(h["bytes"], h["kernel_us"] * 1e-6)
+    traffic = measured_traffic() if not args.only or args.only == "32k" else None
+    result = dict(
+        metric=METRIC, value=round(value, 1), unit="GB/s", n_gpus=1, steps=h["steps"],
+        warmup=args.warmup, ms_per_step=round(h["ms"], 5), us_per_step=round(h["ms"] * 1e3, 2),
+        pct_of_peak=round(100 * value / PEAK_GBS, 1), higher_is_better=True, scaling="weak",
+        vs_baseline=None, dtype="f16", data="synthetic N(0,1) q/K/V, seeded, shuffled pages",
+        config={"workload": name, "B": len(lens), "L": lens[0], "Hq": 32, "Hkv": 8,
+                "head_dim": 128, "page": 16, "seed": 11, "accumulate": "f32",
+                "path": "pdattn_plan_run (balanced single launch)", "workgroups": h["workgroups"],
+                "algorithmic_bytes": h["bytes"], "cache_flush_bytes": FLUSH_BYTES,
+                "timing": "median of per-step HIP events, 1 GiB read flush before each step"},
+        roofline={"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                  "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
+                  "kernel": "decode_streamk_kernel", "kernel_us": round(h["kernel_us"], 2),
+                  "timing": f"{h['kernel_launches']} back-to-back launches over {h['kv_copies']} "
+                            f"K/V copies (>= 1 GiB) between one event pair"},
         device={"arch": dinfo.arch.decode(), "cus": dinfo.compute_units},
     )
-    del t, ws, keep_un
-    torch.cuda.empty_cache()
-
-    if not args.no_secondary:
+    if "uniform" in h:
+        result["uniform_path"] = h["uniform"]
+    if not args.only and not args.no_secondary:
         sec = {}
         ceil = ceiling_gbs(timer, args.steps)
         result["stream_read_ceiling_GBs"] = round(ceil, 1)
-        result["pct_of_ceiling"] = round(100 * gbs / ceil, 1)
-        bt2, t2 = make_device_batch([1024] * 64, 32, 8, seed=11)
-        f2, plan2, ws2 = streamk_runner(bt2, t2, s)
-        w2 = timer.run([f2], args.steps, args.warmup)[0]
-        m2 = statistics.median(w2)
-        b2 = bt2.algorithmic_bytes()
-        sec["64x1K"] = {"us_per_step": round(m2 * 1e3, 2), "GB/s": round(b2 / (m2 * 1e-3) / 1e9, 1),
-                        "pct_of_peak": round(100 * b2 / (m2 * 1e-3) / 1e9 / PEAK_GBS, 1),
-                        "pct_of_ceiling": round(100 * b2 / (m2 * 1e-3) / 1e9 / ceil, 1),
-                        "workgroups": plan2.info().workgroups, "algorithmic_bytes": b2}
-        del t2, ws2
-        torch.cuda.empty_cache()
-        # cascade: 64 requests x (8192 shared + 512 private) vs the non-shared kernel
-        bt3, t3 = make_device_batch(None, 32, 8, seed=21, shared_prefix=8192, suffix=[512] * 64)
-        f3n, plan3, ws3 = streamk_runner(bt3, t3, s)
-        base = pdattn.make_params(t3["q"], t3["k"], t3["v"], t3["indptr"], t3["indices"], t3["last"],
-                                  bt3.B, 32, 8)
-        cp = pdattn.CascadePlan(base, bt3.indptr, bt3.indices, bt3.lens, t3["indices"])
-        cws = pdattn.Workspace()
-        cp.decode(t3["out"], t3["lse"], cws, s)  # uploads the schedule
-        f3c = lambda: cp.decode(t3["out"], t3["lse"], cws, s)  # noqa: E731
-        w3n, w3c = timer.run([f3n, f3c], args.steps, args.warmup, rounds=3)
-        mn, mc = statistics.median(w3n), statistics.median(w3c)
-        ci = cp.info()
-        sec["cascade_64x(8192+512)"] = {
-            "non_shared_us": round(mn * 1e3, 2), "cascade_us": round(mc * 1e3, 2),
-            "speedup": round(mn / mc, 2), "prefix_chunks": ci.prefix_chunks,
-            "prefix_workgroups": ci.prefix_workgroups, "suffix_workgroups": ci.suffix_workgroups}
-        cp.close()
-        pdattn.workspace_release(cws)
+        result["pct_of_ceiling"] = round(100 * value / ceil, 1)
+        result["roofline"]["frac_of_ceiling"] = round(achieved / ceil, 4)
+        h2 = decode_workload(timer, [1024] * 64, args, with_uniform=False)
+        v2, a2 = gbs(h2["bytes"], h2["ms"] * 1e-3), gbs(h2["bytes"], h2["kernel_us"] * 1e-6)
+        sec["64x1K"] = {"us_per_step": round(h2["ms"] * 1e3, 2), "GB/s": round(v2, 1),
+                        "pct_of_peak": round(100 * v2 / PEAK_GBS, 1),
+                        "pct_of_ceiling": round(100 * v2 / ceil, 1),
+                        "kernel_us": round(h2["kernel_us"], 2), "kernel_GB/s": round(a2, 1),
+                        "kernel_frac_of_ceiling": round(a2 / ceil, 4),
+                        "workgroups": h2["workgroups"], "algorithmic_bytes": h2["bytes"]}
+        sec["cascade_64x(8192+512)"] = cascade_workload(timer, args)
         result["secondary"] = sec
-
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not args.only:
         result["cpu_baseline"] = cpu_baseline([32768], 32, 8, seed=11)
     else:
         result["cpu_baseline"] = None

@@ -6,22 +6,23 @@
 // as a normalized partial (o, lse), then a log-sum-exp merge of the partials.
 //
 // How it maps to CDNA4:
-//  * A workgroup is 4 waves; all of them work on one (sequence, kv head) token range, each wave
-//    on every 4th page of it. K and V rows go straight from HBM into VGPRs with 16-byte loads:
-//    a 256-byte row (128 fp16) is read by LPR lanes, so one wave-wide load instruction reads
-//    64/LPR rows of one page, each as whole 128-byte lines. No LDS staging is needed because
-//    every lane reads only the bytes it computes with.
+//  * A workgroup is 8 waves; all of them work on one (sequence, kv head) token range, each wave
+//    on every 8th page of it. K and V rows go straight from HBM into VGPRs with 16-byte
+//    non-temporal loads: a 256-byte row (128 fp16) is read by LPR lanes, so one wave-wide load
+//    instruction reads 64/LPR rows of one page, each as whole 128-byte lines. No LDS staging is
+//    needed because every lane reads only the bytes it computes with.
 //  * Scores: each lane takes the fp16 dot product of its slice of q_h and k_j with
 //    v_dot2_f32_f16 (fp32 accumulate), then the LPR lanes of a row sum with DPP row ops
 //    (quad_perm, row_half_mirror, row_mirror), which leaves the score in every lane of the row.
 //  * Every lane therefore owns whole keys: it keeps its own online-softmax state (max, sum,
 //    output slice) over the keys it holds, so the PV product needs no cross-lane traffic. The
-//    64/LPR independent states of a wave are merged once at the end with shuffles, and the four
-//    waves of the workgroup through LDS.
+//    64/LPR independent states of a wave are merged once at the end in the VALU (DPP row_ror and
+//    v_permlane16/32_swap), and the eight waves of the workgroup through LDS.
 //  * Softmax runs in base 2 on log2(e)-prescaled scores with v_exp_f32 / v_log_f32
 //    (exp(x) = 2^(x log2 e)); the running output is rescaled only when some lane's max grows
 //    (a wave-uniform branch), which after the first pages is rare.
-//  * Prefetch: the loads of the next page are issued before the current page is computed.
+//  * Prefetch: a two-page ring in VGPRs; the loads of the next page are issued before the
+//    current page is computed.
 //
 // Lane geometry, G = query heads per kv head:
 //   G <= 4: LPR = 8 lanes per row, 8 rows per load, each lane holds 2 rows x 16 dims of a page;
@@ -653,21 +654,11 @@ int occupancy_of(const void* fn, int threads) {
     return n > 0 ? n : 1;
 }
 
-// Kernel shapes: the default per G, plus G = 4 alternatives selected by PDATTN_VARIANT while
-// tuning.
+// Kernel shape per group size G: 8 lanes per 256-byte row (16 for G = 8, which needs the
+// registers), 8 waves, and a two-page ring. Deeper rings (3, 4, 6 pages), 16 lanes per row for
+// G = 4 and 4-wave workgroups measured within a few percent of this shape on MI355X.
 template <int G>
 using DefaultCfg = Cfg<G, (G >= 8 ? 16 : 8), 8, 2>;
-using V1 = Cfg<4, 8, 8, 3>;
-using V2 = Cfg<4, 16, 8, 3>;
-using V3 = Cfg<4, 16, 8, 4>;
-using V4 = Cfg<4, 16, 4, 4>;
-using V5 = Cfg<4, 8, 4, 3>;
-using V6 = Cfg<4, 16, 4, 6>;
-
-int variant_env() {
-    const char* v = getenv("PDATTN_VARIANT");
-    return v ? atoi(v) : 0;
-}
 
 template <class C>
 void launch_p(const PartialArgs& a, hipStream_t s) {
@@ -682,38 +673,20 @@ int occ_p() { return occupancy_of(reinterpret_cast<const void*>(&decode_partial_
 template <class C>
 int occ_s() { return occupancy_of(reinterpret_cast<const void*>(&decode_streamk_kernel<C>), C::NT); }
 
-#define PD_DISPATCH(G, FN, ...)                                  \
-    do {                                                         \
-        if ((G) == 4) {                                          \
-            switch (variant_env()) {                             \
-                case 1: FN<V1>(__VA_ARGS__); break;              \
-                case 2: FN<V2>(__VA_ARGS__); break;              \
-                case 3: FN<V3>(__VA_ARGS__); break;              \
-                case 4: FN<V4>(__VA_ARGS__); break;              \
-                case 5: FN<V5>(__VA_ARGS__); break;              \
-                case 6: FN<V6>(__VA_ARGS__); break;              \
-                default: FN<DefaultCfg<4>>(__VA_ARGS__); break;  \
-            }                                                    \
-        } else if ((G) == 1) FN<DefaultCfg<1>>(__VA_ARGS__);     \
-        else if ((G) == 2) FN<DefaultCfg<2>>(__VA_ARGS__);       \
-        else FN<DefaultCfg<8>>(__VA_ARGS__);                     \
+#define PD_DISPATCH(G, FN, ...)                              \
+    do {                                                     \
+        if ((G) == 1) FN<DefaultCfg<1>>(__VA_ARGS__);        \
+        else if ((G) == 2) FN<DefaultCfg<2>>(__VA_ARGS__);   \
+        else if ((G) == 4) FN<DefaultCfg<4>>(__VA_ARGS__);   \
+        else FN<DefaultCfg<8>>(__VA_ARGS__);                 \
     } while (0)
 
-#define PD_DISPATCH_RET(G, FN)                                   \
-    do {                                                         \
-        if ((G) == 4) {                                          \
-            switch (variant_env()) {                             \
-                case 1: return FN<V1>();                         \
-                case 2: return FN<V2>();                         \
-                case 3: return FN<V3>();                         \
-                case 4: return FN<V4>();                         \
-                case 5: return FN<V5>();                         \
-                case 6: return FN<V6>();                         \
-                default: return FN<DefaultCfg<4>>();             \
-            }                                                    \
-        } else if ((G) == 1) return FN<DefaultCfg<1>>();         \
-        else if ((G) == 2) return FN<DefaultCfg<2>>();           \
-        return FN<DefaultCfg<8>>();                              \
+#define PD_DISPATCH_RET(G, FN)                               \
+    do {                                                     \
+        if ((G) == 1) return FN<DefaultCfg<1>>();            \
+        if ((G) == 2) return FN<DefaultCfg<2>>();            \
+        if ((G) == 4) return FN<DefaultCfg<4>>();            \
+        return FN<DefaultCfg<8>>();                          \
     } while (0)
 
 }  // namespace
