@@ -317,12 +317,13 @@ def main():
         vs_baseline=None, dtype="f16", data="synthetic N(0,1) q/K/V, seeded, shuffled pages",
         config={"workload": name, "B": len(lens), "L": lens[0], "Hq": 32, "Hkv": 8,
                 "head_dim": 128, "page": 16, "seed": 11, "accumulate": "f32",
-                "path": "pdattn_plan_run (balanced single launch)", "workgroups": h["workgroups"],
+                "path": "pdattn_plan_run (balanced decode launch + merge launch for split pairs)", "workgroups": h["workgroups"],
                 "algorithmic_bytes": h["bytes"], "cache_flush_bytes": FLUSH_BYTES,
                 "timing": "median of per-step HIP events, 1 GiB read flush before each step"},
         roofline={"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                   "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
-                  "kernel": "decode_streamk_kernel", "kernel_us": round(h["kernel_us"], 2),
+                  "kernel": "decode_balanced_kernel (+ merge_split_kernel when pairs are split)",
+                  "kernel_us": round(h["kernel_us"], 2),
                   "timing": f"{h['kernel_launches']} back-to-back launches over {h['kv_copies']} "
                             f"K/V copies (>= 1 GiB) between one event pair"},
         device={"arch": dinfo.arch.decode(), "cus": dinfo.compute_units},

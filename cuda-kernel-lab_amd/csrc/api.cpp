@@ -46,6 +46,9 @@ int hip_fail(hipError_t e, const char* what) {
     } while (0)
 
 constexpr size_t kAlign = 256;
+constexpr int kDefaultChunkPages = 64;
+static_assert(PDATTN_SCHEDULE_SEGMENTS == kSegMax && PDATTN_SCHEDULE_WG_INTS == kBalDescInts,
+              "schedule layout in pdattn.h matches the kernel's descriptor");
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -56,7 +59,7 @@ bool valid_group(int G) { return G == 1 || G == 2 || G == 4 || G == 8; }
 struct DeviceFacts {
     int cus = 0;
     int occ_partial[9] = {};
-    int occ_streamk[9] = {};
+    int occ_balanced[9] = {};
     int occ_prefix[9] = {};
     char arch[64] = {};
 };
@@ -77,7 +80,7 @@ int device_facts(DeviceFacts* out) {
         snprintf(f.arch, sizeof f.arch, "%s", prop.gcnArchName);
         for (int G : {1, 2, 4, 8}) {
             f.occ_partial[G] = occupancy_decode_partial(G);
-            f.occ_streamk[G] = occupancy_decode_streamk(G);
+            f.occ_balanced[G] = occupancy_decode_balanced(G);
             f.occ_prefix[G] = occupancy_cascade_prefix(G);
         }
     }
@@ -164,12 +167,12 @@ int ensure_ws(pdattn_workspace* ws, size_t need) {
 
 struct pdattn_plan {
     int B = 0, Hq = 0, Hkv = 0, G = 0;
-    int nnz = 0, jbase = 0, W = 1, n_empty = 0;
+    int nnz = 0, jbase = 0, W = 1, P = 16;
     int64_t U = 0;
-    int split_pairs = 0, max_contrib = 0;
+    int split_pairs = 0, max_contrib = 0, n_entries = 0, n_slots = 0, segments = 0;
     // workspace layout (bytes from the base)
-    size_t off_desc = 0, off_empty = 0, off_cnt = 0, off_plse = 0, off_po = 0, ws_bytes = 0;
-    std::vector<int32_t> host_blob;   // desc[W * kDescInts] followed by empty_seq[n_empty]
+    size_t off_desc = 0, off_list = 0, off_plse = 0, off_po = 0, ws_bytes = 0;
+    std::vector<int32_t> host_blob;   // desc[W * kBalDescInts] followed by the merge list
     void* pinned = nullptr;           // pinned copy of host_blob for stream-ordered upload
     size_t blob_bytes = 0;
     const void* uploaded_to = nullptr;
@@ -190,17 +193,22 @@ struct pdattn_cascade_plan {
 
 namespace {
 
-// Balanced split of the flattened (kv head, page) units over W workgroups; see pdattn.h.
-// Units are pages in kv-head-major order: unit u is page-table position (u mod nnz) of kv head
-// (u / nnz). Workgroup w owns units [U w / W, U (w+1) / W). The walk below cuts each range into
-// segments at sequence boundaries and records, per segment, everything the kernel needs, so the
-// kernel never reads kv_indptr / kv_last_page_len. W grows (doubling) until every workgroup has
-// at most kSegMax segments and kRangeMax pages.
-int build_streamk_plan(const int32_t* indptr, const int32_t* last, int B, int Hq, int Hkv,
-                       int force_wg, pdattn_plan* pl) {
+// Balanced split; see pdattn.h and pdattn_internal.h. Chunks of up to P pages of one (sequence,
+// kv head) pair are ordered sequence-major, then by chunk position, kv head fastest, so that any
+// stretch of the order mixes all kv heads (whose K/V rows sit at different offsets of every page,
+// which the memory system serves at different rates). Workgroup w owns the units
+// [U w / W, U (w+1) / W) of that order; the walk below cuts each range into one segment per chunk
+// piece. The contributors of a pair are its segments in unit order; a pair with more than one
+// (or every pair, when `merge_all` is set for extra partials) gets consecutive partial slots and
+// an entry in the merge list. W grows (doubling) until every workgroup has at most kSegMax
+// segments and kRangeMax pages.
+int build_balanced_plan(const int32_t* indptr, const int32_t* last, int B, int Hq, int Hkv,
+                        int force_wg, int chunk_pages, bool merge_all, pdattn_plan* pl) {
     int G = 0;
     if (int st = check_heads(Hq, Hkv, &G)) return st;
     if (B < 0) return fail(PDATTN_ERR_INVALID_ARGUMENT, "B=%d is negative", B);
+    if (chunk_pages < 0 || chunk_pages > kRangeMax)
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "chunk_pages=%d outside [0, %d]", chunk_pages, kRangeMax);
     if (B > 0)
         if (int st = check_host_table(indptr, last, B)) return st;
 
@@ -208,86 +216,116 @@ int build_streamk_plan(const int32_t* indptr, const int32_t* last, int B, int Hq
     pl->Hq = Hq;
     pl->Hkv = Hkv;
     pl->G = G;
+    pl->P = chunk_pages > 0 ? chunk_pages : kDefaultChunkPages;
     pl->jbase = B > 0 ? indptr[0] : 0;
     pl->nnz = B > 0 ? indptr[B] - indptr[0] : 0;
     pl->U = (int64_t)Hkv * pl->nnz;
-    std::vector<int32_t> empty;
-    for (int b = 0; b < B; ++b)
-        if (indptr[b + 1] == indptr[b]) empty.push_back(b);
-    pl->n_empty = (int)empty.size();
 
-    // grid: one full wave of resident workgroups (runtime occupancy x CUs), never more
+    // grid: one workgroup per CU (the kernel's four waves take one SIMD each), never more
     // workgroups than page units; a forced size needs no device query
     int64_t W = force_wg;
     if (W <= 0) {
         DeviceFacts f;
         if (int st = device_facts(&f)) return st;
-        W = (int64_t)f.cus * std::max(1, f.occ_streamk[G]);
-        if (pl->U == 0) W = std::min<int64_t>(W, f.cus);
+        W = f.cus;
     }
-    if (pl->U == 0) W = std::max<int64_t>(1, std::min<int64_t>(W, (int64_t)pl->n_empty * Hkv));
-    else W = std::max<int64_t>(1, std::min<int64_t>(W, pl->U));
+    W = std::max<int64_t>(1, std::min<int64_t>(W, std::max<int64_t>(1, pl->U)));
     W = std::max<int64_t>(W, (pl->U + kRangeMax - 1) / kRangeMax);
     if (W > (1 << 28)) return fail(PDATTN_ERR_INVALID_ARGUMENT, "grid too large");
 
-    const int64_t U = pl->U, nnz = pl->nnz;
+    const int64_t U = pl->U;
+    const int P = pl->P;
     auto seq_len = [&](int b) { return (indptr[b + 1] - indptr[b] - 1) * kPage + last[b]; };
+    const size_t pairs = (size_t)B * Hkv;
+    struct SegRef { int64_t w; int idx; size_t pair; };
     std::vector<int32_t> desc;
+    std::vector<SegRef> refs;
+    std::vector<int> nc;
     for (;;) {
-        desc.assign((size_t)W * kDescInts, 0);
+        desc.assign((size_t)W * kBalDescInts, 0);
+        refs.clear();
+        nc.assign(pairs, 0);
         bool ok = true;
-        int split = 0, mx = 1;
-        for (int64_t w = 0; w < W && ok && U > 0; ++w) {
-            const int64_t u0 = U * w / W, u1 = U * (w + 1) / W;
-            if (u1 - u0 > kRangeMax) { ok = false; break; }
-            int32_t* d = &desc[(size_t)w * kDescInts];
-            int nseg = 0;
-            for (int64_t u = u0; u < u1;) {
-                const int kvh = (int)(u / nnz);
-                const int j = (int)(u % nnz);
-                // the non-empty sequence holding position j: first b with indptr[b+1] - jbase > j
-                const int b = (int)(std::upper_bound(indptr + 1, indptr + B + 1, j + pl->jbase) - (indptr + 1));
-                const int pb = indptr[b] - pl->jbase, pe = indptr[b + 1] - pl->jbase;
-                const int64_t seg_end = std::min<int64_t>(u1, (int64_t)kvh * nnz + pe);
-                if (nseg == kSegMax) { ok = false; break; }
-                const int64_t uf = (int64_t)kvh * nnz + pb, ul = uf + (pe - pb) - 1;
-                const int64_t w1 = ((uf + 1) * W - 1) / U, w2 = ((ul + 1) * W - 1) / U;
-                int32_t* sg = d + 8 + kSegInts * nseg;
-                sg[0] = b;
-                sg[1] = kvh;
-                sg[2] = (int)(u - u0);
-                sg[3] = (int)(seg_end - u);
-                sg[4] = (j - pb) * kPage;
-                sg[5] = (seg_end - (int64_t)kvh * nnz == pe) ? seq_len(b) : (int)(seg_end - (int64_t)kvh * nnz - pb) * kPage;
-                sg[6] = (int)w1;
-                sg[7] = (int)(w2 - w1 + 1);
-                if (w == w1 && w2 > w1) ++split;
-                mx = std::max(mx, (int)(w2 - w1 + 1));
-                ++nseg;
-                u = seg_end;
+        int64_t w = 0, u = 0;
+        int64_t wbeg = 0, wend = U / W;
+        for (int b = 0; b < B && ok; ++b) {
+            const int np = indptr[b + 1] - indptr[b];
+            for (int pa = 0; pa < np && ok; pa += P) {
+                const int pn = std::min(P, np - pa);
+                for (int kvh = 0; kvh < Hkv && ok; ++kvh) {
+                    for (int done = 0; done < pn;) {
+                        while (u >= wend) {
+                            ++w;
+                            wbeg = wend;
+                            wend = U * (w + 1) / W;
+                        }
+                        if (wend - wbeg > kRangeMax) { ok = false; break; }
+                        const int take = (int)std::min<int64_t>(pn - done, wend - u);
+                        int32_t* d = &desc[(size_t)w * kBalDescInts];
+                        if (d[0] == kSegMax) { ok = false; break; }
+                        int32_t* sg = d + 8 + kSegInts * d[0];
+                        const int p0 = pa + done, p1 = pa + done + take;
+                        sg[0] = b;
+                        sg[1] = kvh;
+                        sg[2] = (int)(u - wbeg);
+                        sg[3] = take;
+                        sg[4] = p0 * kPage;
+                        sg[5] = p1 == np ? seq_len(b) : p1 * kPage;
+                        sg[6] = indptr[b] - pl->jbase + p0;
+                        sg[7] = -1;
+                        const size_t pr = (size_t)b * Hkv + kvh;
+                        refs.push_back({w, d[0], pr});
+                        ++nc[pr];
+                        ++d[0];
+                        u += take;
+                        done += take;
+                    }
+                }
             }
-            d[0] = nseg;
         }
-        if (ok) {
-            pl->split_pairs = split;
-            pl->max_contrib = mx;
-            break;
-        }
+        if (ok) break;
         if (W >= U) return fail(PDATTN_ERR_INVALID_ARGUMENT, "cannot partition the batch");
         W = std::min<int64_t>(U, W * 2);
     }
-    pl->W = (int)W;
-    pl->host_blob = desc;
-    pl->host_blob.insert(pl->host_blob.end(), empty.begin(), empty.end());
 
-    const size_t pairs = (size_t)B * Hkv;
-    const size_t slots = pairs + (size_t)pl->W;
+    // partial slots and merge list: pairs in (b, kv head) order, contributors in unit order
+    std::vector<int32_t> slot0(pairs, -1), list;
+    int slots = 0, split = 0, mx = 1;
+    auto need_slots = [&](size_t pr) { return nc[pr] > 1 || (merge_all && nc[pr] > 0); };
+    for (int b = 0; b < B; ++b)
+        for (int kvh = 0; kvh < Hkv; ++kvh) {
+            const size_t pr = (size_t)b * Hkv + kvh;
+            if (nc[pr] > 1) ++split;
+            mx = std::max(mx, nc[pr]);
+            if (need_slots(pr)) {
+                slot0[pr] = slots;
+                slots += nc[pr];
+                list.insert(list.end(), {b, kvh, slot0[pr], nc[pr]});
+            } else if (nc[pr] == 0) {
+                list.insert(list.end(), {b, kvh, 0, 0});   // empty sequence: extras only, or 0 / -inf
+            }
+        }
+    std::vector<int> seen(pairs, 0);
+    for (const SegRef& rf : refs) {
+        int32_t* sg = &desc[(size_t)rf.w * kBalDescInts + 8 + kSegInts * rf.idx];
+        const int k = seen[rf.pair]++;
+        if (need_slots(rf.pair)) sg[7] = slot0[rf.pair] + k;
+    }
+
+    pl->W = (int)W;
+    pl->split_pairs = split;
+    pl->max_contrib = mx;
+    pl->n_entries = (int)(list.size() / 4);
+    pl->n_slots = slots;
+    pl->segments = (int)refs.size();
+    pl->host_blob = desc;
+    pl->host_blob.insert(pl->host_blob.end(), list.begin(), list.end());
+
     size_t off = 0;
     pl->off_desc = off;  off += align_up(sizeof(int32_t) * desc.size());
-    pl->off_empty = off; off += align_up(sizeof(int32_t) * std::max(1, pl->n_empty));
-    pl->off_cnt = off;   off += align_up(sizeof(int32_t) * std::max<size_t>(1, pairs));
-    pl->off_plse = off;  off += align_up(sizeof(float) * slots * G);
-    pl->off_po = off;    off += align_up(sizeof(float) * slots * G * kHeadDim);
+    pl->off_list = off;  off += align_up(sizeof(int32_t) * std::max<size_t>(4, list.size()));
+    pl->off_plse = off;  off += align_up(sizeof(float) * std::max(1, slots) * G);
+    pl->off_po = off;    off += align_up(sizeof(float) * std::max(1, slots) * G * kHeadDim);
     pl->ws_bytes = off;
     pl->blob_bytes = sizeof(int32_t) * pl->host_blob.size();
     return PDATTN_OK;
@@ -300,34 +338,33 @@ void free_plan_storage(pdattn_plan* pl) {
     }
 }
 
-int upload_streamk(pdattn_plan* pl, void* ws, size_t bytes, hipStream_t s) {
+int upload_plan(pdattn_plan* pl, void* ws, size_t bytes, hipStream_t s) {
     if (!ws) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null workspace");
     if (bytes < pl->ws_bytes)
         return fail(PDATTN_ERR_WORKSPACE, "workspace holds %zu bytes, plan needs %zu", bytes, pl->ws_bytes);
     char* base = static_cast<char*>(ws);
-    const size_t desc_bytes = sizeof(int32_t) * (size_t)pl->W * kDescInts;
+    const size_t desc_bytes = sizeof(int32_t) * (size_t)pl->W * kBalDescInts;
     if (pl->blob_bytes && !pl->pinned) {
-        // pinned staging copy, made once: the copy below is stream-ordered and asynchronous
+        // pinned staging copy, made once: the copies below are stream-ordered and asynchronous
         hipError_t e = hipHostMalloc(&pl->pinned, pl->blob_bytes, hipHostMallocDefault);
         if (e != hipSuccess) return hip_fail(e, "hipHostMalloc(plan)");
         std::memcpy(pl->pinned, pl->host_blob.data(), pl->blob_bytes);
     }
     if (pl->blob_bytes) {
         PD_HIP(hipMemcpyAsync(base + pl->off_desc, pl->pinned, desc_bytes, hipMemcpyHostToDevice, s));
-        if (pl->n_empty)
-            PD_HIP(hipMemcpyAsync(base + pl->off_empty, static_cast<char*>(pl->pinned) + desc_bytes,
-                                  sizeof(int32_t) * pl->n_empty, hipMemcpyHostToDevice, s));
+        if (pl->n_entries)
+            PD_HIP(hipMemcpyAsync(base + pl->off_list, static_cast<char*>(pl->pinned) + desc_bytes,
+                                  sizeof(int32_t) * 4 * pl->n_entries, hipMemcpyHostToDevice, s));
     }
-    const size_t pairs = (size_t)pl->B * pl->Hkv;
-    PD_HIP(launch_fill_i32(reinterpret_cast<int32_t*>(base + pl->off_cnt), 0, std::max<size_t>(1, pairs), s));
     pl->uploaded_to = ws;
     return PDATTN_OK;
 }
 
-int run_streamk(const pdattn_plan* pl, const void* q, const void* k, const void* v,
-                const int32_t* indptr, const int32_t* indices, const int32_t* last, float sm_scale,
-                void* out, float* lse, void* ws, size_t bytes, hipStream_t s,
-                const float* extra_o = nullptr, const float* extra_lse = nullptr, int n_extra = 0) {
+// Balanced decode launch, then (when the plan lists any) the merge launch.
+int run_plan(const pdattn_plan* pl, const void* q, const void* k, const void* v,
+             const int32_t* indptr, const int32_t* indices, const int32_t* last, float sm_scale,
+             void* out, float* lse, void* ws, size_t bytes, hipStream_t s,
+             const float* extra_o = nullptr, const float* extra_lse = nullptr, int n_extra = 0) {
     if (ws != pl->uploaded_to)
         return fail(PDATTN_ERR_NOT_READY, "plan was not uploaded into this workspace");
     if (bytes < pl->ws_bytes)
@@ -339,31 +376,40 @@ int run_streamk(const pdattn_plan* pl, const void* q, const void* k, const void*
         return fail(PDATTN_ERR_INVALID_ARGUMENT, "q / k_cache / v_cache / out must be 16-byte aligned");
     if (!std::isfinite(sm_scale)) return fail(PDATTN_ERR_INVALID_ARGUMENT, "sm_scale is not finite");
     char* base = static_cast<char*>(ws);
-    StreamKArgs a;
-    a.q = static_cast<const _Float16*>(q);
-    a.k = static_cast<const uint8_t*>(k);
-    a.v = static_cast<const uint8_t*>(v);
-    a.kv_indices = indices;
-    a.out = static_cast<_Float16*>(out);
-    a.lse = lse;
-    a.desc = reinterpret_cast<const int32_t*>(base + pl->off_desc);
-    a.empty_seq = reinterpret_cast<const int32_t*>(base + pl->off_empty);
-    a.counters = reinterpret_cast<int32_t*>(base + pl->off_cnt);
-    a.part_lse = reinterpret_cast<float*>(base + pl->off_plse);
-    a.part_o = reinterpret_cast<float*>(base + pl->off_po);
-    a.extra_o = extra_o;
-    a.extra_lse = extra_lse;
-    a.n_extra = n_extra;
-    a.U = pl->U;
-    a.nnz = pl->nnz;
-    a.jbase = pl->jbase;
-    a.B = pl->B;
-    a.Hq = pl->Hq;
-    a.Hkv = pl->Hkv;
-    a.W = pl->W;
-    a.n_empty = pl->n_empty;
-    a.scale_log2 = sm_scale * 1.4426950408889634f;
-    PD_HIP(launch_decode_streamk(a, pl->G, s));
+    float* part_lse = reinterpret_cast<float*>(base + pl->off_plse);
+    float* part_o = reinterpret_cast<float*>(base + pl->off_po);
+    if (pl->U > 0) {
+        BalArgs a;
+        a.q = static_cast<const _Float16*>(q);
+        a.k = static_cast<const uint8_t*>(k);
+        a.v = static_cast<const uint8_t*>(v);
+        a.kv_indices = indices + pl->jbase;
+        a.out = static_cast<_Float16*>(out);
+        a.lse = lse;
+        a.desc = reinterpret_cast<const int32_t*>(base + pl->off_desc);
+        a.part_o = part_o;
+        a.part_lse = part_lse;
+        a.B = pl->B;
+        a.Hq = pl->Hq;
+        a.Hkv = pl->Hkv;
+        a.W = pl->W;
+        a.scale_log2 = sm_scale * 1.4426950408889634f;
+        PD_HIP(launch_decode_balanced(a, pl->G, s));
+    }
+    if (pl->n_entries) {
+        MergeArgs m;
+        m.list = reinterpret_cast<const int32_t*>(base + pl->off_list);
+        m.part_o = part_o;
+        m.part_lse = part_lse;
+        m.extra_o = extra_o;
+        m.extra_lse = extra_lse;
+        m.out = static_cast<_Float16*>(out);
+        m.lse = lse;
+        m.Hq = pl->Hq;
+        m.G = pl->G;
+        m.n_extra = n_extra;
+        PD_HIP(launch_merge_split(m, pl->n_entries, s));
+    }
     return PDATTN_OK;
 }
 
@@ -500,12 +546,13 @@ int pdattn_decode_attention(const pdattn_decode_params* p, int G, int variant, v
 }
 
 int pdattn_plan_create(const int32_t* h_kv_indptr, const int32_t* h_kv_last_page_len, int B,
-                       int Hq, int Hkv, int force_workgroups, pdattn_plan** plan) {
+                       int Hq, int Hkv, int force_workgroups, int chunk_pages, pdattn_plan** plan) {
     if (!plan) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null plan output");
     *plan = nullptr;
     if (B > 0 && !h_kv_indptr) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null kv_indptr");
     pdattn_plan* pl = new pdattn_plan();
-    if (int st = build_streamk_plan(h_kv_indptr, h_kv_last_page_len, B, Hq, Hkv, force_workgroups, pl)) {
+    if (int st = build_balanced_plan(h_kv_indptr, h_kv_last_page_len, B, Hq, Hkv, force_workgroups,
+                                     chunk_pages, false, pl)) {
         free_plan_storage(pl);
         delete pl;
         return st;
@@ -522,6 +569,18 @@ int pdattn_plan_get_info(const pdattn_plan* pl, pdattn_plan_info* info) {
     info->max_contributors = pl->max_contrib;
     info->units = pl->U;
     info->workspace_bytes = pl->ws_bytes;
+    info->chunk_pages = pl->P;
+    info->segments = pl->segments;
+    info->merge_entries = pl->n_entries;
+    info->schedule_ints = (int)pl->host_blob.size();
+    return PDATTN_OK;
+}
+
+int pdattn_plan_get_schedule(const pdattn_plan* pl, int32_t* out, size_t count) {
+    if (!pl || !out) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null pointer");
+    if (count < pl->host_blob.size())
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "schedule holds %zu ints, %zu given", pl->host_blob.size(), count);
+    std::memcpy(out, pl->host_blob.data(), sizeof(int32_t) * pl->host_blob.size());
     return PDATTN_OK;
 }
 
@@ -529,7 +588,7 @@ size_t pdattn_plan_workspace_size(const pdattn_plan* pl) { return pl ? pl->ws_by
 
 int pdattn_plan_upload(pdattn_plan* pl, void* workspace, size_t bytes, void* stream) {
     if (!pl) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null plan");
-    return upload_streamk(pl, workspace, bytes, static_cast<hipStream_t>(stream));
+    return upload_plan(pl, workspace, bytes, static_cast<hipStream_t>(stream));
 }
 
 int pdattn_plan_run(const pdattn_plan* pl, const void* q, const void* k_cache, const void* v_cache,
@@ -537,8 +596,8 @@ int pdattn_plan_run(const pdattn_plan* pl, const void* q, const void* k_cache, c
                     const int32_t* kv_last_page_len, float sm_scale, void* out, float* lse,
                     void* workspace, size_t bytes, void* stream) {
     if (!pl) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null plan");
-    return run_streamk(pl, q, k_cache, v_cache, kv_indptr, kv_indices, kv_last_page_len, sm_scale,
-                       out, lse, workspace, bytes, static_cast<hipStream_t>(stream));
+    return run_plan(pl, q, k_cache, v_cache, kv_indptr, kv_indices, kv_last_page_len, sm_scale,
+                    out, lse, workspace, bytes, static_cast<hipStream_t>(stream));
 }
 
 void pdattn_plan_destroy(pdattn_plan* pl) {
@@ -637,7 +696,7 @@ int pdattn_cascade_plan_create(const pdattn_decode_params* base, const int32_t* 
     cp->use = (cp->Lp > 0 && cp->Lp >= min_prefix) ? 1 : 0;
     int st = PDATTN_OK;
     if (!cp->use) {
-        st = build_streamk_plan(h_indptr, last.data(), B, base->Hq, base->Hkv, 0, &cp->sk);
+        st = build_balanced_plan(h_indptr, last.data(), B, base->Hq, base->Hkv, 0, 0, false, &cp->sk);
         cp->off_sk = 0;
         cp->ws_bytes = cp->sk.ws_bytes;
     } else {
@@ -658,7 +717,7 @@ int pdattn_cascade_plan_create(const pdattn_decode_params* base, const int32_t* 
             for (int i = h_indptr[b] + P; i < h_indptr[b + 1]; ++i) sidx.push_back(h_indices[i]);
             sind[b + 1] = (int32_t)sidx.size();
         }
-        st = build_streamk_plan(sind.data(), last.data(), B, base->Hq, base->Hkv, 0, &cp->sk);
+        st = build_balanced_plan(sind.data(), last.data(), B, base->Hq, base->Hkv, 0, 0, true, &cp->sk);
         cp->tbl = sind;
         cp->tbl.insert(cp->tbl.end(), sidx.begin(), sidx.end());
         const size_t rows = (size_t)B * base->Hq;
@@ -706,11 +765,11 @@ int pdattn_cascade_decode(pdattn_cascade_plan* cp, void* out, float* lse, pdattn
         if (cp->use)
             PD_HIP(hipMemcpyAsync(base + cp->off_tbl, cp->pinned, cp->tbl.size() * sizeof(int32_t),
                                   hipMemcpyHostToDevice, s));
-        if (int st = upload_streamk(&cp->sk, base + cp->off_sk, cp->sk.ws_bytes, s)) return st;
+        if (int st = upload_plan(&cp->sk, base + cp->off_sk, cp->sk.ws_bytes, s)) return st;
         cp->uploaded_to = ws->base;
     }
     if (!cp->use)
-        return run_streamk(&cp->sk, p.q, p.k_cache, p.v_cache, p.kv_indptr, p.kv_indices,
+        return run_plan(&cp->sk, p.q, p.k_cache, p.v_cache, p.kv_indptr, p.kv_indices,
                            p.kv_last_page_len, p.sm_scale, out, lse, base + cp->off_sk, cp->sk.ws_bytes, s);
     float* ppo = reinterpret_cast<float*>(base + cp->off_ppo);
     float* pplse = reinterpret_cast<float*>(base + cp->off_pplse);
@@ -731,7 +790,7 @@ int pdattn_cascade_decode(pdattn_cascade_plan* cp, void* out, float* lse, pdattn
     if (int st = pdattn_cascade_prefix(&pp, stream)) return st;
     const int32_t* sind = reinterpret_cast<const int32_t*>(base + cp->off_tbl);
     const int32_t* sidx = sind + (p.B + 1);
-    return run_streamk(&cp->sk, p.q, p.k_cache, p.v_cache, sind, sidx, p.kv_last_page_len, p.sm_scale,
+    return run_plan(&cp->sk, p.q, p.k_cache, p.v_cache, sind, sidx, p.kv_last_page_len, p.sm_scale,
                        out, lse, base + cp->off_sk, cp->sk.ws_bytes, s, ppo, pplse, cp->cpre);
 }
 
@@ -765,7 +824,7 @@ int pdattn_get_device_info(pdattn_device_info* info) {
     DeviceFacts f;
     if (int st = device_facts(&f)) return st;
     info->compute_units = f.cus;
-    info->decode_wg_per_cu = f.occ_streamk[4];
+    info->decode_wg_per_cu = f.occ_balanced[4];
     info->prefix_wg_per_cu = f.occ_prefix[4];
     snprintf(info->arch, sizeof info->arch, "%s", f.arch);
     return PDATTN_OK;

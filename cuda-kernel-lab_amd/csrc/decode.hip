@@ -83,9 +83,10 @@ __device__ __forceinline__ float row_sum(float v) {
 // r and r^1 for the 16-lane swap, r and r^2 for the 32-lane swap), always in the same order, so
 // r0 + r1 is bitwise the same in all lanes. The second operand is passed through an empty asm
 // statement: given the same SSA value twice, the compiler treats the two results as equal and
-// drops the second one.
+// drops the second one. The statement is not volatile, so the many independent reductions of a
+// merge can still be interleaved by the scheduler.
 __device__ __forceinline__ unsigned opaque_copy(unsigned v) {
-    asm volatile("" : "+v"(v));
+    asm("" : "+v"(v));
     return v;
 }
 template <bool ROWS32>
@@ -147,9 +148,6 @@ struct Smem {
     float o[NW][G][kHeadDim];
     float fo[G][kHeadDim];    // combined, normalized output of the workgroup
     float flse[G];            // combined lse (natural log)
-    float wmax[NW][G];        // merge scratch: per-wave maxima,
-    float gmax[G];            //   per-row maximum,
-    float red[NW * 64 * 6];   //   per-thread partial states
 };
 
 template <class C>
@@ -356,7 +354,7 @@ __device__ __forceinline__ void process_range(Smem<C::G, C::NW>& sm, const _Floa
 // loop, where they would spill. The kernarg-segment intrinsic is only valid in the kernel body
 // itself (in a called function it evaluates to null), so kargs() is called only from the kernel
 // and the pointer is passed down to the (force-inlined) helpers.
-typedef const __attribute__((address_space(4))) StreamKArgs* KArgPtr;
+typedef const __attribute__((address_space(4))) BalArgs* KArgPtr;
 __device__ __forceinline__ KArgPtr kargs() {
     KArgPtr p = (KArgPtr)__builtin_amdgcn_kernarg_segment_ptr();
     asm volatile("" : "+s"(p));
@@ -386,75 +384,39 @@ __device__ __forceinline__ void lse_accumulate(float& m, float& ws, float4& acc,
     acc.w = fmaf(w, o.w, acc.w);
 }
 
-// Log-sum-exp merge of the G rows of one (sequence, kv head) pair from a list of sources, in a
-// fixed source order (deterministic whatever order the sources were produced in):
-//   source 0 (if `own`): the workgroup's own result in LDS (sm.fo / sm.flse);
-//   then `nslots` stored partials: o at part_o[((s0 + k) * G + h) * 128], lse at part_lse[(s0 + k) * G + h];
-//   then the `n_extra` extra partials of each row: o at extra_o[(row * n_extra + e) * 128], lse at
-//   extra_lse[row * n_extra + e].
-// One pass: each thread owns one 4-dim quad of one row and every TPQ-th source, issues all its
-// loads, accumulates them online, and the TPQ partial states of a quad are combined in order
-// through LDS. Writes fp16 out and fp32 lse; a row whose every source is empty gets 0 / -inf.
-template <int G, int NW, bool ACQUIRE>
-__device__ __forceinline__ void merge_sources(Smem<G, NW>& sm, KArgPtr a, int b, int kvh, bool own,
-                                              int64_t s0, int nslots) {
-    // partials written by other workgroups (write-through atomic stores, completed before their
-    // arrival was counted): drop any stale copies this XCD's caches hold, then plain loads
-    if constexpr (ACQUIRE) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    constexpr int NT = NW * 64;
-    constexpr int Q = G * 32;          // 4-dim quads of the G rows
-    constexpr int TPQ = NT / Q;        // threads per quad
-    static_assert(NT % Q == 0, "thread count must cover the quads");
-    const int tid = threadIdx.x;
-    const int n_extra = a->n_extra;
-    const int nsrc = (own ? 1 : 0) + nslots + n_extra;
-    const size_t row0 = (size_t)b * a->Hq + (size_t)kvh * G;
-    const int quad = tid % Q, r = tid / Q;
-    const int h = quad / 32, d0 = 4 * (quad % 32);
-
-    auto load_src = [&](int k, float& l, float4& o) {
-        if (own) {
-            if (k == 0) {
-                l = sm.flse[h];
-                o = make_float4(sm.fo[h][d0], sm.fo[h][d0 + 1], sm.fo[h][d0 + 2], sm.fo[h][d0 + 3]);
-                return;
-            }
-            --k;
-        }
-        if (k < nslots) {
-            const float* pl = a->part_lse + (s0 + k) * G + h;
-            const float* po = a->part_o + ((s0 + k) * G + h) * kHeadDim + d0;
-            l = *pl;
-            o = *reinterpret_cast<const float4*>(po);
-            return;
-        }
-        const size_t e = (row0 + h) * n_extra + (k - nslots);
-        l = a->extra_lse[e];
-        o = *reinterpret_cast<const float4*>(a->extra_o + e * kHeadDim + d0);
-    };
-
+// Log-sum-exp merge of one row from `nsrc` partial states in a fixed order (merge_states,
+// 01_decode_attention.cu:238-255): each of TPQ threads per 4-dim quad takes every TPQ-th source,
+// issuing four independent 16-byte loads at a time and accumulating them online; the TPQ states
+// of a quad are then combined in thread order through LDS. The result does not depend on the order
+// in which the sources were produced. load(k, l, o) fetches source k's lse and its quad of o. A row
+// whose every source is empty gets out = 0, lse = -inf.
+constexpr int kMergeThreads = 256;
+template <class Load>
+__device__ __forceinline__ void merge_row(int nsrc, Load load, float* red, _Float16* out_row, float* lse_out) {
+    constexpr int Q = kHeadDim / 4, TPQ = kMergeThreads / Q;
+    const int tid = threadIdx.x, quad = tid % Q, r = tid / Q;
     float m = -INFINITY, ws = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int k = r; k < nsrc; k += 4 * TPQ) {
         float l[4];
         float4 o[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) load_src(min(k + u * TPQ, nsrc - 1), l[u], o[u]);
+        for (int u = 0; u < 4; ++u) load(min(k + u * TPQ, nsrc - 1), 4 * quad, l[u], o[u]);
 #pragma unroll
         for (int u = 0; u < 4; ++u)
             if (k + u * TPQ < nsrc) lse_accumulate(m, ws, acc, l[u], o[u]);
     }
-    float* red = sm.red + (size_t)tid * 6;
-    red[0] = m;
-    red[1] = ws;
-    red[2] = acc.x;
-    red[3] = acc.y;
-    red[4] = acc.z;
-    red[5] = acc.w;
+    float* rd = red + tid * 6;
+    rd[0] = m;
+    rd[1] = ws;
+    rd[2] = acc.x;
+    rd[3] = acc.y;
+    rd[4] = acc.z;
+    rd[5] = acc.w;
     __syncthreads();
     if (r == 0) {
         for (int rr = 1; rr < TPQ; ++rr) {
-            const float* o = sm.red + (size_t)(rr * Q + quad) * 6;
+            const float* o = red + (rr * Q + quad) * 6;
             if (o[1] > 0.f) {
                 // fold in a partial state (o[0] + ln o[1], o[2..5] / o[1])
                 const float mm = fmaxf(m, o[0]);
@@ -468,14 +430,13 @@ __device__ __forceinline__ void merge_sources(Smem<G, NW>& sm, KArgPtr a, int b,
             }
         }
         const float inv = ws > 0.f ? 1.f / ws : 0.f;
-        _Float16* out = a->out + (row0 + h) * kHeadDim + d0;
-        out[0] = (_Float16)(acc.x * inv);
-        out[1] = (_Float16)(acc.y * inv);
-        out[2] = (_Float16)(acc.z * inv);
-        out[3] = (_Float16)(acc.w * inv);
-        if (d0 == 0) a->lse[row0 + h] = ws > 0.f ? m + fast_log2(ws) * kLn2 : -INFINITY;
+        _Float16* op = out_row + 4 * quad;
+        op[0] = (_Float16)(acc.x * inv);
+        op[1] = (_Float16)(acc.y * inv);
+        op[2] = (_Float16)(acc.z * inv);
+        op[3] = (_Float16)(acc.w * inv);
+        if (quad == 0) *lse_out = ws > 0.f ? m + fast_log2(ws) * kLn2 : -INFINITY;
     }
-    __syncthreads();
 }
 
 // ---- uniform chunks: the reference's decode_partial launch shape -------------------------
@@ -501,151 +462,302 @@ __global__ __launch_bounds__(C::NT) void decode_partial_kernel(PartialArgs a) {
 }
 
 // ---- log-sum-exp merge: the reference's merge_states launch shape -------------------------
-// One workgroup per row: each of 8 threads per 4-dim quad takes every 8th chunk (independent
-// 16-byte loads, accumulated online), and the 8 states are combined in order through LDS.
-constexpr int kMergeThreads = 256;
+// One workgroup per row, `num_chunks` consecutive partial slots.
 __global__ __launch_bounds__(kMergeThreads) void merge_states_kernel(const float* __restrict__ part_o,
                                                                       const float* __restrict__ part_lse,
                                                                       _Float16* __restrict__ out,
                                                                       float* __restrict__ lse_out,
                                                                       int num_chunks) {
-    constexpr int Q = kHeadDim / 4, TPQ = kMergeThreads / Q;
     __shared__ float red[kMergeThreads * 6];
-    const int row = blockIdx.x, tid = threadIdx.x;
-    const float* pl = part_lse + (size_t)row * num_chunks;
-    const float* po = part_o + (size_t)row * num_chunks * kHeadDim;
-    const int quad = tid % Q, r = tid / Q, d0 = 4 * quad;
-    float m = -INFINITY, ws = 0.f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int c = r; c < num_chunks; c += 4 * TPQ) {
-        float l[4];
-        float4 o[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int cc = min(c + u * TPQ, num_chunks - 1);
-            l[u] = pl[cc];
-            o[u] = *reinterpret_cast<const float4*>(po + (size_t)cc * kHeadDim + d0);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (c + u * TPQ < num_chunks) lse_accumulate(m, ws, acc, l[u], o[u]);
-    }
-    float* rd = red + tid * 6;
-    rd[0] = m;
-    rd[1] = ws;
-    rd[2] = acc.x;
-    rd[3] = acc.y;
-    rd[4] = acc.z;
-    rd[5] = acc.w;
-    __syncthreads();
-    if (r == 0) {
-        for (int rr = 1; rr < TPQ; ++rr) {
-            const float* o = red + (rr * Q + quad) * 6;
-            if (o[1] > 0.f) {
-                const float mm = fmaxf(m, o[0]);
-                const float sa = fast_exp2((m - mm) * kLog2e), sb = fast_exp2((o[0] - mm) * kLog2e);
-                ws = ws * sa + o[1] * sb;
-                acc.x = acc.x * sa + o[2] * sb;
-                acc.y = acc.y * sa + o[3] * sb;
-                acc.z = acc.z * sa + o[4] * sb;
-                acc.w = acc.w * sa + o[5] * sb;
-                m = mm;
-            }
-        }
-        const float inv = ws > 0.f ? 1.f / ws : 0.f;
-        _Float16* op = out + (size_t)row * kHeadDim + d0;
-        op[0] = (_Float16)(acc.x * inv);
-        op[1] = (_Float16)(acc.y * inv);
-        op[2] = (_Float16)(acc.z * inv);
-        op[3] = (_Float16)(acc.w * inv);
-        if (quad == 0) lse_out[row] = ws > 0.f ? m + fast_log2(ws) * kLn2 : -INFINITY;
-    }
+    const size_t row = blockIdx.x;
+    const float* pl = part_lse + row * num_chunks;
+    const float* po = part_o + row * num_chunks * kHeadDim;
+    merge_row(num_chunks,
+              [&](int k, int d0, float& l, float4& o) {
+                  l = pl[k];
+                  o = *reinterpret_cast<const float4*>(po + (size_t)k * kHeadDim + d0);
+              },
+              red, out + row * kHeadDim, lse_out + row);
 }
 
-// ---- balanced single launch ------------------------------------------------------------------
-// Hand-off of a split pair's partials between workgroups, possibly on different XCDs (whose L2
-// caches are not coherent with each other): contributors write their partial with agent-scope
-// atomic stores (write-through to the coherent level), wait until those stores have completed
-// (s_waitcnt), then count themselves in with an agent-scope atomic add; the last contributor
-// invalidates its own caches once (agent-scope acquire) and reads the partials with plain
-// vector loads. No L2 write-back (which __threadfence() would issue in every contributing
-// workgroup, flushing and invalidating that XCD's whole L2) is needed.
+// ---- balanced launch -------------------------------------------------------------------------
+// Merge of the pairs listed by the planner: one workgroup per row (entry, head). Sources: the
+// pair's partial slots in order, then the row's extra partials (cascade prefix chunks).
+__global__ __launch_bounds__(kMergeThreads) void merge_split_kernel(MergeArgs a) {
+    __shared__ float red[kMergeThreads * 6];
+    const int e = blockIdx.x / a.G, h = blockIdx.x % a.G;
+    const int b = a.list[4 * e], kvh = a.list[4 * e + 1], slot0 = a.list[4 * e + 2], nc = a.list[4 * e + 3];
+    const int G = a.G, n_extra = a.n_extra;
+    const size_t row = (size_t)b * a.Hq + (size_t)kvh * G + h;
+    merge_row(nc + n_extra,
+              [&](int k, int d0, float& l, float4& o) {
+                  if (k < nc) {
+                      const size_t sl = (size_t)(slot0 + k) * G + h;
+                      l = a.part_lse[sl];
+                      o = *reinterpret_cast<const float4*>(a.part_o + sl * kHeadDim + d0);
+                  } else {
+                      const size_t ex = row * n_extra + (k - nc);
+                      l = a.extra_lse[ex];
+                      o = *reinterpret_cast<const float4*>(a.extra_o + ex * kHeadDim + d0);
+                  }
+              },
+              red, a.out + row * kHeadDim, a.lse + row);
+}
+
+// A page of one kv head seen through a buffer resource: base = cache + page * page_bytes +
+// kvh * 256, num_records = the bytes from there to the end of the page, so every lane's offset is
+// in range. A padding slot of the ring uses num_records = 0: its loads return zeros without a
+// memory access, while the ring still issues the same loads in every slot (exact wait counts).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const uint8_t* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
 template <class C>
-__global__ __launch_bounds__(C::NT) void decode_streamk_kernel(StreamKArgs a) {
-    constexpr int G = C::G, NW = C::NW, NT = C::NT;
-    __shared__ Smem<G, NW> sm;
-    __shared__ int pg[kRangeMax];
-    __shared__ int s_last;
-    const int w = blockIdx.x, tid = threadIdx.x;
-
-    // Sequences without pages: the result is the merge of the extra partials alone (0 / -inf
-    // when there are none).
-    for (int e = w; e < kargs()->n_empty * a.Hkv; e += a.W)
-        merge_sources<G, NW, false>(sm, kargs(), kargs()->empty_seq[e / a.Hkv], e % a.Hkv, false, 0, 0);
-
-    const int64_t u0 = a.U * w / a.W, u1 = a.U * (w + 1) / a.W;
-    const int R = (int)(u1 - u0);
-    if (R <= 0) return;
-    // page ids of this workgroup's range: units u0 .. u1-1 of the kv-head-major order are the
-    // consecutive page-table positions (u mod nnz), so they load before any descriptor arrives
-    for (int qq = tid; qq < R; qq += NT)
-        pg[qq] = a.kv_indices[a.jbase + (int)((u0 + qq) % a.nnz)];
-    const int nseg = kargs()->desc[(size_t)w * kDescInts];
-    __syncthreads();
-
-    for (int si = 0; si < nseg; ++si) {
-        const int32_t* sg = kargs()->desc + (size_t)w * kDescInts + 8 + kSegInts * si;
-        const int b = sg[0], kvh = sg[1], qa = sg[2], t0 = sg[4], t1 = sg[5];
-        process_range<C>(sm, a.q + ((size_t)b * a.Hq + kvh * G) * kHeadDim, a.k, a.v, pg + qa, t0,
-                         t0, t1, a.Hkv, kvh, a.scale_log2);
-        const int32_t* sg2 = kargs()->desc + (size_t)w * kDescInts + 8 + kSegInts * si;
-        const int w1 = sg2[6], nc = sg2[7];
-        if (nc == 1) {
-            // the whole (sequence, kv head) pair was ours: final result
-            if (kargs()->n_extra == 0) {
-                for (int idx = tid; idx < G * kHeadDim; idx += NT) {
-                    const int h = idx / kHeadDim, d = idx % kHeadDim;
-                    const size_t row = (size_t)b * a.Hq + kvh * G + h;
-                    kargs()->out[row * kHeadDim + d] = (_Float16)sm.fo[h][d];
-                    if (d == 0) kargs()->lse[row] = sm.flse[h];
-                }
-            } else {
-                merge_sources<G, NW, false>(sm, kargs(), b, kvh, true, 0, 0);
-            }
-        } else {
-            // one of nc contributors: store the partial with agent-scope atomic stores, count
-            // arrivals; the last one merges all nc partials in workgroup order
-            const int p = kvh * a.B + b;
-            const size_t slot = (size_t)p + w;
-            for (int idx = tid; idx < G * kHeadDim; idx += NT) {
-                const int h = idx / kHeadDim, d = idx % kHeadDim;
-                __hip_atomic_store(kargs()->part_o + (slot * G + h) * kHeadDim + d, sm.fo[h][d],
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (d == 0)
-                    __hip_atomic_store(kargs()->part_lse + slot * G + h, sm.flse[h], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-            }
-            __builtin_amdgcn_s_waitcnt(0);   // this thread's partial stores have completed
-            __syncthreads();
-            if (tid == 0) {
-                const int old = __hip_atomic_fetch_add(&kargs()->counters[p], 1, __ATOMIC_RELAXED,
-                                                       __HIP_MEMORY_SCOPE_AGENT);
-                s_last = (old == nc - 1) ? 1 : 0;
-            }
-            __syncthreads();
-            if (s_last) {
-                merge_sources<G, NW, true>(sm, kargs(), b, kvh, false, (int64_t)p + w1, nc);
-                if (tid == 0)
-                    __hip_atomic_store(&kargs()->counters[p], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+__device__ __forceinline__ void load_page_rsrc(PageRegs<C>& pr, __amdgpu_buffer_rsrc_t rk,
+                                               __amdgpu_buffer_rsrc_t rv, uint32_t lbase, uint32_t rstride) {
+#pragma unroll
+    for (int i = 0; i < C::RG; ++i)
+#pragma unroll
+        for (int kk = 0; kk < C::PPL; ++kk) {
+            const int off = (int)(lbase + i * rstride + kk * (C::LPR * 16));
+            // aux = 2: non-temporal (K/V bytes are read once)
+            pr.k[i][kk] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 2);
+            pr.v[i][kk] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 2);
         }
-        __syncthreads();  // sm is reused by the next segment
+}
+
+// Per-segment merge scratch of the balanced kernel: the raw online-softmax state of every row
+// group of every wave (NS = waves x row groups sources), then per-source weights. o rows are
+// padded by 4 floats so that the row groups of a wave, which write the same columns, fall in
+// different LDS banks.
+template <int G, int NS>
+struct BalSmem {
+    static constexpr int OP = kHeadDim + 4;
+    float m[NS][G];
+    float l[NS][G];
+    float o[NS][G][OP];
+    float alpha[NS][G];       // exp(m_src - M) per source and head
+    float rinv[G];            // 1 / L
+    float lse[G];
+};
+
+template <class C>
+__device__ __forceinline__ void reset_state(WaveState<C>& st) {
+#pragma unroll
+    for (int h = 0; h < C::G; ++h) {
+        st.m[h] = -INFINITY;
+        st.l[h] = 0.f;
+#pragma unroll
+        for (int d = 0; d < C::DPL; ++d) st.o[h][d] = 0.f;
     }
 }
 
-__global__ void fill_i32_kernel(int32_t* p, int32_t value, size_t n) {
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        p[i] = value;
+// End of a segment. Every row group of every wave is one source state (max, sum, output slice);
+// all of them go to LDS unmerged, one wave turns the per-source maxima into weights, and every
+// thread forms its outputs as one weighted sum over the sources, in source order. Writes the G
+// rows as the final fp16 out / lse (slot < 0) or as partial slot `slot` (normalized o, lse).
+template <class C>
+__device__ __forceinline__ void flush_segment(BalSmem<C::G, C::NW * C::RPI>& sm, WaveState<C>& st,
+                                              KArgPtr a, size_t row0, int slot) {
+    constexpr int G = C::G, NT = C::NT, LPR = C::LPR, NS = C::NW * C::RPI;
+    // one wave computes the source weights: lane = s * G + h covers sources s + j * SL, j < J
+    constexpr int SL = 64 / G, J = (NS + SL - 1) / SL;
+    const int tid = threadIdx.x, lane = tid & 63, c = lane % LPR;
+    const int src = (tid >> 6) * C::RPI + lane / LPR;
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+        for (int kk = 0; kk < C::PPL; ++kk) {
+            float4* dst = reinterpret_cast<float4*>(&sm.o[src][h][(kk * LPR + c) * 8]);
+            dst[0] = make_float4(st.o[h][kk * 8 + 0], st.o[h][kk * 8 + 1], st.o[h][kk * 8 + 2], st.o[h][kk * 8 + 3]);
+            dst[1] = make_float4(st.o[h][kk * 8 + 4], st.o[h][kk * 8 + 5], st.o[h][kk * 8 + 6], st.o[h][kk * 8 + 7]);
+        }
+    if (c == 0) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            sm.m[src][h] = st.m[h];
+            sm.l[src][h] = st.l[h];
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const int s0 = tid / G, h = tid % G;
+        float mv[J];
+        float M = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int s = s0 + j * SL;
+            mv[j] = s < NS ? sm.m[s][h] : -INFINITY;
+            M = fmaxf(M, mv[j]);
+        }
+#pragma unroll
+        for (int off = G; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
+        float L = 0.f;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int s = s0 + j * SL;
+            const float al = (mv[j] == -INFINITY) ? 0.f : fast_exp2(mv[j] - M);
+            if (s < NS) {
+                sm.alpha[s][h] = al;
+                L = fmaf(al, sm.l[s][h], L);
+            }
+        }
+#pragma unroll
+        for (int off = G; off < 64; off <<= 1) L += __shfl_xor(L, off);
+        if (tid < G) {
+            sm.rinv[h] = L > 0.f ? 1.f / L : 0.f;
+            sm.lse[h] = L > 0.f ? (M + fast_log2(L)) * kLn2 : -INFINITY;
+        }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < G * kHeadDim; idx += NT) {
+        const int h = idx / kHeadDim, d = idx % kHeadDim;
+        float O = 0.f;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) O = fmaf(sm.alpha[s][h], sm.o[s][h][d], O);
+        const float val = O * sm.rinv[h];
+        if (slot < 0) {
+            a->out[(row0 + h) * kHeadDim + d] = (_Float16)val;
+            if (d == 0) a->lse[row0 + h] = sm.lse[h];
+        } else {
+            a->part_o[((size_t)slot * G + h) * kHeadDim + d] = val;
+            if (d == 0) a->part_lse[(size_t)slot * G + h] = sm.lse[h];
+        }
+    }
+    __syncthreads();   // sm is reused by the next segment
+}
+
+// One workgroup of 4 waves (one per SIMD) per CU walks its list of segments. Wave i takes pages
+// i, i+4, ... of each segment; its pages of all segments form one stream, each segment's share
+// padded to a multiple of the ring depth NBUF so that a page's ring slot is fixed at compile
+// time. The ring runs across segment boundaries: the next segment's first pages are in flight
+// while a segment is flushed. Partials are written with plain stores and merged by a second
+// kernel, so no workgroup waits for another.
+template <class C>
+__global__ __launch_bounds__(C::NT) void decode_balanced_kernel(BalArgs a) {
+    constexpr int G = C::G, NW = C::NW, NT = C::NT, NBUF = C::NBUF, LPR = C::LPR;
+    __shared__ BalSmem<G, NW * C::RPI> sm;
+    __shared__ int pg[kRangeMax];
+    __shared__ int sd[kSegMax * kSegInts];
+    __shared__ u32x4 qs[kSegMax][G * kHeadDim / 8];
+    // the wave index is made wave-uniform explicitly: everything the page ring derives from it
+    // (per-wave page counts, page ids, buffer resources) must live in scalar registers
+    const int w = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane / LPR, c = lane % LPR;
+    // Segment fields are read from LDS and made wave-uniform: global (vector) loads of them would
+    // count against the same wait counter as the ring's page loads, and a non-uniform value in a
+    // buffer resource would turn every page load into a loop over lanes.
+    auto fld = [&](int si, int f) { return __builtin_amdgcn_readfirstlane(sd[si * kSegInts + f]); };
+
+    const int32_t* desc = kargs()->desc + (size_t)w * kBalDescInts;
+    const int nseg = __builtin_amdgcn_readfirstlane(desc[0]);
+    if (nseg <= 0) return;   // uniform: the planner gives every workgroup at least one segment
+    for (int i = tid; i < nseg * kSegInts; i += NT) sd[i] = desc[8 + i];
+    __syncthreads();
+    // page ids and q rows of every segment into LDS: all loads are issued before any is stored
+    // (one round trip, not one per segment). Item i < npages is page i of the workgroup's list,
+    // found in the segment whose range [qa, qa + npg) holds it; q item j is 16 bytes of the
+    // G q rows of segment j / (G*16).
+    {
+        constexpr int PMAX = kRangeMax / NT, QPS = G * kHeadDim / 8, QMAX = (kSegMax * QPS + NT - 1) / NT;
+        const int npages = fld(nseg - 1, 2) + fld(nseg - 1, 3);
+        int pv[PMAX];
+        u32x4 qv4[QMAX];
+#pragma unroll
+        for (int k = 0; k < PMAX; ++k) {
+            const int i = tid + k * NT;
+            pv[k] = 0;
+            if (i < npages) {
+                int si = 0;
+                while (si + 1 < nseg && sd[(si + 1) * kSegInts + 2] <= i) ++si;
+                pv[k] = kargs()->kv_indices[sd[si * kSegInts + 6] + (i - sd[si * kSegInts + 2])];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < QMAX; ++k) {
+            const int j = tid + k * NT;
+            if (j < nseg * QPS) {
+                const int si = j / QPS;
+                const size_t row = (size_t)sd[si * kSegInts] * a.Hq + (size_t)sd[si * kSegInts + 1] * G;
+                qv4[k] = reinterpret_cast<const u32x4*>(kargs()->q + row * kHeadDim)[j % QPS];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < PMAX; ++k)
+            if (tid + k * NT < npages) pg[tid + k * NT] = pv[k];
+#pragma unroll
+        for (int k = 0; k < QMAX; ++k)
+            if (tid + k * NT < nseg * QPS) qs[(tid + k * NT) / QPS][(tid + k * NT) % QPS] = qv4[k];
+    }
+    __syncthreads();
+
+    const uint32_t page_bytes = (uint32_t)(kPage * a.Hkv * 256);
+    const uint32_t lbase = (uint32_t)(r * a.Hkv * 256 + c * 16);
+    const uint32_t rstride = (uint32_t)(C::RPI * a.Hkv * 256);
+    auto wcount = [&](int npg) { return npg > wave ? (npg - wave + NW - 1) / NW : 0; };
+
+    // prefetch cursor: segment ps, slot pslot of this wave's (padded) share pcnt / ppad
+    int ps = 0, pslot = 0, pcnt = 0, ppad = 0;
+    auto seek = [&]() {
+        while (ps < nseg) {
+            pcnt = wcount(fld(ps, 3));
+            ppad = (pcnt + NBUF - 1) / NBUF * NBUF;
+            if (ppad > 0) break;
+            ++ps;
+        }
+    };
+    seek();
+    auto issue = [&](PageRegs<C>& buf) {
+        const uint8_t* kb = kargs()->k;
+        const uint8_t* vb = kargs()->v;
+        uint32_t nrec = 0;
+        if (ps < nseg && pslot < pcnt) {
+            const int kvh = fld(ps, 1);
+            const int pid = __builtin_amdgcn_readfirstlane(pg[fld(ps, 2) + wave + NW * pslot]);
+            const size_t off = (size_t)(uint32_t)pid * page_bytes + (size_t)kvh * 256;
+            kb += off;
+            vb += off;
+            nrec = page_bytes - (uint32_t)kvh * 256;
+        }
+        load_page_rsrc<C>(buf, page_rsrc(kb, nrec), page_rsrc(vb, nrec), lbase, rstride);
+        if (ps < nseg && ++pslot == ppad) {
+            ++ps;
+            pslot = 0;
+            seek();
+        }
+    };
+
+    PageRegs<C> buf[NBUF];
+#pragma unroll
+    for (int u = 0; u < NBUF - 1; ++u) issue(buf[u]);
+
+    WaveState<C> st;
+    reset_state<C>(st);
+    for (int si = 0; si < nseg; ++si) {
+        const int npg = fld(si, 3), t0 = fld(si, 4), t1 = fld(si, 5);
+        f16x2 qv[G][C::PPL][4];
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int kk = 0; kk < C::PPL; ++kk) {
+                const u32x4 raw = qs[si][h * (kHeadDim / 8) + kk * LPR + c];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) qv[h][kk][e] = as_h2(raw[e]);
+            }
+        const int cnt = wcount(npg);
+        for (int blk = 0; blk < cnt; blk += NBUF) {
+#pragma unroll
+            for (int u = 0; u < NBUF; ++u) {
+                issue(buf[(u + NBUF - 1) % NBUF]);
+                if (blk + u < cnt)
+                    page_step<C>(st, buf[u], qv, t0 + (wave + NW * (blk + u)) * kPage + r, t0, t1,
+                                 a.scale_log2);
+            }
+        }
+        flush_segment<C>(sm, st, kargs(), (size_t)fld(si, 0) * a.Hq + (size_t)fld(si, 1) * G, fld(si, 7));
+        reset_state<C>(st);
+    }
 }
 
 int occupancy_of(const void* fn, int threads) {
@@ -654,46 +766,53 @@ int occupancy_of(const void* fn, int threads) {
     return n > 0 ? n : 1;
 }
 
-// Kernel shape per group size G: 8 lanes per 256-byte row (16 for G = 8, which needs the
-// registers), 8 waves, and a two-page ring. Deeper rings (3, 4, 6 pages), 16 lanes per row for
-// G = 4 and 4-wave workgroups measured within a few percent of this shape on MI355X.
+// Kernel shapes per group size G.
+// Uniform split (reference launch shape): 8 lanes per 256-byte row (16 for G = 8, which needs the
+// registers), 8 waves, a two-page ring.
 template <int G>
-using DefaultCfg = Cfg<G, (G >= 8 ? 16 : 8), 8, 2>;
+using PartialCfg = Cfg<G, (G >= 8 ? 16 : 8), 8, 2>;
+// Balanced launch: 4 waves (one per SIMD, one workgroup per CU), 16 lanes per row (four row groups
+// per wave, so the end-of-segment merge is two permlane steps), a four-page ring.
+#ifndef PD_BAL_NBUF
+#define PD_BAL_NBUF 4
+#endif
+template <int G>
+using BalCfg = Cfg<G, 16, 4, (G >= 8 ? 3 : PD_BAL_NBUF)>;
 
 template <class C>
 void launch_p(const PartialArgs& a, hipStream_t s) {
     decode_partial_kernel<C><<<dim3(a.num_chunks, a.B * a.Hkv), C::NT, 0, s>>>(a);
 }
 template <class C>
-void launch_s(const StreamKArgs& a, hipStream_t s) {
-    decode_streamk_kernel<C><<<a.W, C::NT, 0, s>>>(a);
+void launch_b(const BalArgs& a, hipStream_t s) {
+    decode_balanced_kernel<C><<<a.W, C::NT, 0, s>>>(a);
 }
 template <class C>
 int occ_p() { return occupancy_of(reinterpret_cast<const void*>(&decode_partial_kernel<C>), C::NT); }
 template <class C>
-int occ_s() { return occupancy_of(reinterpret_cast<const void*>(&decode_streamk_kernel<C>), C::NT); }
+int occ_b() { return occupancy_of(reinterpret_cast<const void*>(&decode_balanced_kernel<C>), C::NT); }
 
-#define PD_DISPATCH(G, FN, ...)                              \
+#define PD_DISPATCH(CFG, G, FN, ...)                         \
     do {                                                     \
-        if ((G) == 1) FN<DefaultCfg<1>>(__VA_ARGS__);        \
-        else if ((G) == 2) FN<DefaultCfg<2>>(__VA_ARGS__);   \
-        else if ((G) == 4) FN<DefaultCfg<4>>(__VA_ARGS__);   \
-        else FN<DefaultCfg<8>>(__VA_ARGS__);                 \
+        if ((G) == 1) FN<CFG<1>>(__VA_ARGS__);               \
+        else if ((G) == 2) FN<CFG<2>>(__VA_ARGS__);          \
+        else if ((G) == 4) FN<CFG<4>>(__VA_ARGS__);          \
+        else FN<CFG<8>>(__VA_ARGS__);                        \
     } while (0)
 
-#define PD_DISPATCH_RET(G, FN)                               \
+#define PD_DISPATCH_RET(CFG, G, FN)                          \
     do {                                                     \
-        if ((G) == 1) return FN<DefaultCfg<1>>();            \
-        if ((G) == 2) return FN<DefaultCfg<2>>();            \
-        if ((G) == 4) return FN<DefaultCfg<4>>();            \
-        return FN<DefaultCfg<8>>();                          \
+        if ((G) == 1) return FN<CFG<1>>();                   \
+        if ((G) == 2) return FN<CFG<2>>();                   \
+        if ((G) == 4) return FN<CFG<4>>();                   \
+        return FN<CFG<8>>();                                 \
     } while (0)
 
 }  // namespace
 
 hipError_t launch_decode_partial(const PartialArgs& a, int G, hipStream_t s) {
     if (G != 1 && G != 2 && G != 4 && G != 8) return hipErrorInvalidValue;
-    PD_DISPATCH(G, launch_p, a, s);
+    PD_DISPATCH(PartialCfg, G, launch_p, a, s);
     return hipGetLastError();
 }
 
@@ -704,20 +823,19 @@ hipError_t launch_merge_states(const float* part_o, const float* part_lse, _Floa
     return hipGetLastError();
 }
 
-hipError_t launch_decode_streamk(const StreamKArgs& a, int G, hipStream_t s) {
+hipError_t launch_decode_balanced(const BalArgs& a, int G, hipStream_t s) {
     if (G != 1 && G != 2 && G != 4 && G != 8) return hipErrorInvalidValue;
-    PD_DISPATCH(G, launch_s, a, s);
+    PD_DISPATCH(BalCfg, G, launch_b, a, s);
     return hipGetLastError();
 }
 
-hipError_t launch_fill_i32(int32_t* p, int32_t value, size_t n, hipStream_t s) {
-    if (n == 0) return hipSuccess;
-    const int grid = (int)std::min<size_t>((n + 255) / 256, 1024);
-    fill_i32_kernel<<<grid, 256, 0, s>>>(p, value, n);
+hipError_t launch_merge_split(const MergeArgs& a, int n_entries, hipStream_t s) {
+    if (n_entries <= 0) return hipSuccess;
+    merge_split_kernel<<<n_entries * a.G, kMergeThreads, 0, s>>>(a);
     return hipGetLastError();
 }
 
-int occupancy_decode_partial(int G) { PD_DISPATCH_RET(G, occ_p); }
-int occupancy_decode_streamk(int G) { PD_DISPATCH_RET(G, occ_s); }
+int occupancy_decode_partial(int G) { PD_DISPATCH_RET(PartialCfg, G, occ_p); }
+int occupancy_decode_balanced(int G) { PD_DISPATCH_RET(BalCfg, G, occ_b); }
 
 }  // namespace pdattn

@@ -25,37 +25,47 @@ struct PartialArgs {
     float scale_log2;         // sm_scale * log2(e)
 };
 
-// Balanced single-launch kernel: per-workgroup descriptor written by the host planner.
-// desc[w * kDescInts + 0] = number of segments; segment s at desc[w * kDescInts + 8 + 8 s] =
-//   {b, kvh, qa, npg, t0, t1, w1, nc}: sequence b, kv head kvh, pages [qa, qa + npg) of the
-//   workgroup's page range, tokens [t0, t1) of the sequence (t0 is the first token of page qa),
-//   first contributing workgroup w1 and contributor count nc of the (b, kvh) pair (nc = 1: this
-//   workgroup covers the whole pair).
-constexpr int kSegMax = 8;                 // segments per workgroup
+// Balanced decode: the host planner cuts the batch into chunks of up to `chunk_pages` pages of
+// one (sequence, kv head) pair, ordered sequence-major, then by chunk position, with the kv head
+// varying fastest, and gives workgroup w the units [U w / W, U (w+1) / W) of that order (a unit is
+// one page of one kv head). Each workgroup's range is cut into segments (one per chunk piece),
+// described in desc[w * kBalDescInts ..]:
+//   desc[0] = number of segments; segment s at desc[8 + kSegInts * s] =
+//   {b, kvh, qa, npg, t0, t1, jpos, slot}: sequence b, kv head kvh, pages [qa, qa + npg) of the
+//   workgroup's page list, tokens [t0, t1) of the sequence (t0 = first token of its first page),
+//   page-table position jpos of its first page (relative to kv_indptr[0]), and the partial slot
+//   it writes (-1: the segment is the whole pair and writes the final out / lse).
+constexpr int kSegMax = 24;                // segments per workgroup
 constexpr int kSegInts = 8;
-constexpr int kDescInts = 8 + kSegMax * kSegInts;
+constexpr int kBalDescInts = 8 + kSegMax * kSegInts;
 constexpr int kRangeMax = 2048;            // pages per workgroup (page ids staged in LDS)
 
-struct StreamKArgs {
+struct BalArgs {
     const _Float16* q;
     const uint8_t*  k;
     const uint8_t*  v;
-    const int32_t*  kv_indices;
+    const int32_t*  kv_indices;   // offset by kv_indptr[0]
     _Float16*       out;
     float*          lse;
-    const int32_t*  desc;         // [W * kDescInts]
-    const int32_t*  empty_seq;    // [n_empty] sequences with no pages
-    int32_t*        counters;     // [B*Hkv] arrival counters of split pairs (zero between launches)
-    float*          part_o;       // [(B*Hkv + W) * G * 128] partial slots, slot = pair + workgroup
-    float*          part_lse;     // [(B*Hkv + W) * G]
-    // extra partials merged into every row (cascade prefix): [B*Hq, n_extra] slots
-    const float*    extra_o;
-    const float*    extra_lse;
-    int64_t U;                    // Hkv * nnz page units, kv-head-major
-    int nnz, jbase;               // pages in the table, kv_indptr[0]
-    int B, Hq, Hkv, W, n_empty;
-    int n_extra;
-    float scale_log2;
+    const int32_t*  desc;         // [W * kBalDescInts]
+    float*          part_o;       // [slots * G * 128] partial outputs (normalized)
+    float*          part_lse;     // [slots * G]
+    int B, Hq, Hkv, W;
+    float scale_log2;             // sm_scale * log2(e)
+};
+
+// Merge of split pairs (and of every pair when extra partials are given): entry e of `list` is
+// {b, kvh, slot0, nc}: the nc >= 0 partial slots slot0 .. slot0 + nc - 1 of the pair, in order,
+// then the n_extra extra partials of each of its G rows.
+struct MergeArgs {
+    const int32_t*  list;         // [n_entries * 4]
+    const float*    part_o;
+    const float*    part_lse;
+    const float*    extra_o;      // [B*Hq, n_extra, 128] or null
+    const float*    extra_lse;    // [B*Hq, n_extra]
+    _Float16*       out;
+    float*          lse;
+    int Hq, G, n_extra;
 };
 
 // Arguments of the MFMA shared-prefix kernel.
@@ -74,7 +84,8 @@ struct PrefixArgs {
 hipError_t launch_decode_partial(const PartialArgs& a, int G, hipStream_t s);
 hipError_t launch_merge_states(const float* part_o, const float* part_lse, _Float16* out,
                                float* lse, int rows, int num_chunks, hipStream_t s);
-hipError_t launch_decode_streamk(const StreamKArgs& a, int G, hipStream_t s);
+hipError_t launch_decode_balanced(const BalArgs& a, int G, hipStream_t s);
+hipError_t launch_merge_split(const MergeArgs& a, int n_entries, hipStream_t s);
 hipError_t launch_fill_i32(int32_t* p, int32_t value, size_t n, hipStream_t s);
 hipError_t launch_cascade_prefix(const PrefixArgs& a, int G, int qtiles, hipStream_t s);
 hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, int grid, hipStream_t s);
@@ -82,7 +93,7 @@ hipError_t launch_flush(void* buf, size_t bytes, int grid, hipStream_t s);
 
 // Occupancy (workgroups per CU) of the kernels, queried from the runtime.
 int occupancy_decode_partial(int G);
-int occupancy_decode_streamk(int G);
+int occupancy_decode_balanced(int G);
 int occupancy_cascade_prefix(int G);
 int prefix_rows_per_workgroup();
 

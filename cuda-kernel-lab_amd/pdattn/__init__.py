@@ -38,7 +38,7 @@ EXPORTS = [
     "pdattn_plan_chunks", "pdattn_decode_partial", "pdattn_merge_states",
     "pdattn_decode_workspace_size", "pdattn_workspace_partials", "pdattn_decode_attention",
     "pdattn_plan_create", "pdattn_plan_get_info", "pdattn_plan_workspace_size",
-    "pdattn_plan_upload", "pdattn_plan_run", "pdattn_plan_destroy",
+    "pdattn_plan_get_schedule", "pdattn_plan_upload", "pdattn_plan_run", "pdattn_plan_destroy",
     "pdattn_shared_prefix_pages", "pdattn_cascade_prefix",
     "pdattn_cascade_plan_create", "pdattn_cascade_plan_get_info", "pdattn_cascade_decode",
     "pdattn_cascade_plan_destroy",
@@ -86,7 +86,9 @@ class PrefixParams(ctypes.Structure):
 class PlanInfo(ctypes.Structure):
     _fields_ = [("workgroups", ctypes.c_int), ("pairs", ctypes.c_int),
                 ("split_pairs", ctypes.c_int), ("max_contributors", ctypes.c_int),
-                ("units", ctypes.c_int64), ("workspace_bytes", ctypes.c_size_t)]
+                ("units", ctypes.c_int64), ("workspace_bytes", ctypes.c_size_t),
+                ("chunk_pages", ctypes.c_int), ("segments", ctypes.c_int),
+                ("merge_entries", ctypes.c_int), ("schedule_ints", ctypes.c_int)]
 
 
 class CascadeInfo(ctypes.Structure):
@@ -132,8 +134,9 @@ def lib():
                                        ctypes.POINTER(P), ctypes.POINTER(P)], I),
         "pdattn_decode_attention": ([ctypes.POINTER(DecodeParams), I, I, P, P,
                                      ctypes.POINTER(Workspace), P], I),
-        "pdattn_plan_create": ([P, P, I, I, I, I, ctypes.POINTER(P)], I),
+        "pdattn_plan_create": ([P, P, I, I, I, I, I, ctypes.POINTER(P)], I),
         "pdattn_plan_get_info": ([P, ctypes.POINTER(PlanInfo)], I),
+        "pdattn_plan_get_schedule": ([P, P, S], I),
         "pdattn_plan_workspace_size": ([P], S),
         "pdattn_plan_upload": ([P, P, S, P], I),
         "pdattn_plan_run": ([P, P, P, P, P, P, P, ctypes.c_float, P, P, P, S, P], I),
@@ -245,22 +248,42 @@ def workspace_release(ws: Workspace):
     lib().pdattn_workspace_release(ctypes.byref(ws))
 
 
-# ---- balanced single-launch path ---------------------------------------------------------------
+# ---- balanced path ---------------------------------------------------------------------------
+
+SCHEDULE_SEGMENTS = 24      # PDATTN_SCHEDULE_SEGMENTS
+SCHEDULE_WG_INTS = 200      # PDATTN_SCHEDULE_WG_INTS
+
 
 class Plan:
-    """pdattn_plan: balanced (stream-K) schedule of one batch, built from host page-table copies."""
+    """pdattn_plan: balanced schedule of one batch, built from host page-table copies."""
 
-    def __init__(self, kv_indptr, kv_last_page_len, B: int, Hq: int, Hkv: int, force_workgroups: int = 0):
+    def __init__(self, kv_indptr, kv_last_page_len, B: int, Hq: int, Hkv: int,
+                 force_workgroups: int = 0, chunk_pages: int = 0):
         self._h = ctypes.c_void_p()
         ip, ipp = host_i32(kv_indptr)
         la, lap = host_i32(kv_last_page_len)
-        _check(lib().pdattn_plan_create(ipp, lap, B, Hq, Hkv, force_workgroups, ctypes.byref(self._h)),
-               "pdattn_plan_create")
+        _check(lib().pdattn_plan_create(ipp, lap, B, Hq, Hkv, force_workgroups, chunk_pages,
+                                        ctypes.byref(self._h)), "pdattn_plan_create")
 
     def info(self) -> PlanInfo:
         inf = PlanInfo()
         _check(lib().pdattn_plan_get_info(self._h, ctypes.byref(inf)), "pdattn_plan_get_info")
         return inf
+
+    def schedule(self):
+        """(segments, merge_list): segments[w] is a list of 8-int segments
+        {b, kvh, qa, npg, t0, t1, jpos, slot}; merge_list is an (n, 4) array {b, kvh, slot0, nc}."""
+        import numpy as np
+        inf = self.info()
+        buf = np.zeros(inf.schedule_ints, dtype=np.int32)
+        _check(lib().pdattn_plan_get_schedule(self._h, buf.ctypes.data_as(ctypes.c_void_p),
+                                              buf.size), "pdattn_plan_get_schedule")
+        W = inf.workgroups
+        segs = []
+        for w in range(W):
+            d = buf[w * SCHEDULE_WG_INTS:(w + 1) * SCHEDULE_WG_INTS]
+            segs.append([d[8 + 8 * i:16 + 8 * i].tolist() for i in range(int(d[0]))])
+        return segs, buf[W * SCHEDULE_WG_INTS:].reshape(-1, 4)
 
     @property
     def workspace_bytes(self) -> int:

@@ -33,6 +33,8 @@ extern "C" {
 
 #define PDATTN_HEAD_DIM 128
 #define PDATTN_PAGE_SIZE 16
+#define PDATTN_SCHEDULE_SEGMENTS 24    /* segments per workgroup in a plan's schedule     */
+#define PDATTN_SCHEDULE_WG_INTS 200    /* int32 per workgroup in a plan's schedule        */
 
 typedef enum pdattn_status {
     PDATTN_OK = 0,
@@ -117,35 +119,53 @@ int pdattn_workspace_partials(const pdattn_workspace* ws, int B, int Hq, int par
 int pdattn_decode_attention(const pdattn_decode_params* p, int G, int variant, void* out,
                             float* lse, pdattn_workspace* ws, void* stream);
 
-/* ---- balanced single-launch path (stream-K plan / run) ----------------------------------- */
-/* The MI355X path for decode_attention: the planner (host, from the host copy of the page
- * table, the way FlashInfer's plan() works) cuts the flattened (kv head, page) work of the whole
- * batch into equal page ranges, one per workgroup of a single full wave over all CUs; ranges
- * cross sequence boundaries freely. A workgroup writes the final out/lse of every sequence it
- * covers completely; a sequence split over several workgroups is merged (fixed order, so the
- * result is deterministic) by the last of them to finish, in the same launch. */
+/* ---- balanced path (plan / run) ---------------------------------------------------------- */
+/* The MI355X path for decode_attention. The planner works on the host, from the host copy of the
+ * page table, the way FlashInfer's plan() does. It cuts every (sequence, kv head) pair into chunks
+ * of up to chunk_pages pages and orders them sequence-major, then by chunk position, with the kv
+ * head varying fastest. It then gives each workgroup of a single launch (one per CU) an equal
+ * range of that order, so every workgroup streams the same number of pages over a mix of kv heads.
+ *
+ * A pair that lies in one workgroup's range is written as the final out / lse by that workgroup.
+ * The pieces of a pair split over several workgroups are written as normalized partials and
+ * merged by a second, small launch, in a fixed order. The result is bitwise deterministic for a
+ * given plan. */
 typedef struct pdattn_plan pdattn_plan;
 
 typedef struct pdattn_plan_info {
-    int     workgroups;        /* grid size W                                             */
+    int     workgroups;        /* grid size W of the decode launch                        */
     int     pairs;             /* B * Hkv                                                 */
-    int     split_pairs;       /* pairs covered by more than one workgroup                */
-    int     max_contributors;  /* most workgroups contributing to one pair                */
-    int64_t units;             /* Hkv * nnz pages                                         */
+    int     split_pairs;       /* pairs covered by more than one segment                  */
+    int     max_contributors;  /* most segments contributing to one pair                  */
+    int64_t units;             /* Hkv * nnz page units                                    */
     size_t  workspace_bytes;
+    int     chunk_pages;       /* pages per chunk                                         */
+    int     segments;          /* segments over all workgroups                            */
+    int     merge_entries;     /* pairs merged by the second launch (0: single launch)    */
+    int     schedule_ints;     /* int32 count of pdattn_plan_get_schedule's output        */
 } pdattn_plan_info;
 
 /* Build a plan from host copies of kv_indptr [B+1] and kv_last_page_len [B]. force_workgroups > 0
- * overrides the occupancy-derived grid size (it is clamped to the number of page units). */
+ * overrides the grid size (one workgroup per CU by default; it is clamped to the number of page
+ * units, and grows when a workgroup would exceed its segment or page limits); chunk_pages > 0
+ * overrides the chunk size (default 64 pages). */
 int pdattn_plan_create(const int32_t* h_kv_indptr, const int32_t* h_kv_last_page_len, int B,
-                       int Hq, int Hkv, int force_workgroups, pdattn_plan** plan);
+                       int Hq, int Hkv, int force_workgroups, int chunk_pages, pdattn_plan** plan);
 int pdattn_plan_get_info(const pdattn_plan* plan, pdattn_plan_info* info);
 size_t pdattn_plan_workspace_size(const pdattn_plan* plan);
-/* Stream-ordered copy of the plan's schedule into `workspace` and reset of its merge counters.
- * Must precede pdattn_plan_run with that workspace; the plan may be run any number of times. */
+/* Copy of the plan's schedule (info.schedule_ints int32): per workgroup, the segment count then
+ * up to 24 segments of 8 ints {b, kvh, offset in the workgroup's page list, pages, first token,
+ * end token, page-table position of the first page (relative to kv_indptr[0]), partial slot or
+ * -1}, 200 ints per workgroup; then the merge list, 4 ints per entry {b, kvh, first slot, slots}.
+ * For inspection and tests; `count` must be at least info.schedule_ints. */
+int pdattn_plan_get_schedule(const pdattn_plan* plan, int32_t* out, size_t count);
+/* Stream-ordered copy of the plan's schedule into `workspace`. Must precede pdattn_plan_run with
+ * that workspace; the plan may then be run any number of times. */
 int pdattn_plan_upload(pdattn_plan* plan, void* workspace, size_t bytes, void* stream);
-/* One launch: attention for every (sequence, q head) of the planned batch. The device page table
- * must hold the same values as the host copy the plan was built from. */
+/* Attention for every (sequence, q head) of the planned batch: the decode launch and, when the
+ * plan has split pairs or empty sequences, the merge launch. The device page table must hold the
+ * same kv_indptr / kv_last_page_len values as the host copy the plan was built from (page ids in
+ * kv_indices may change between runs). */
 int pdattn_plan_run(const pdattn_plan* plan, const void* q, const void* k_cache,
                     const void* v_cache, const int32_t* kv_indptr, const int32_t* kv_indices,
                     const int32_t* kv_last_page_len, float sm_scale, void* out, float* lse,

@@ -1,9 +1,14 @@
-"""The balanced (stream-K) planner -- CPU only.
+"""The balanced planner -- CPU only.
 
-Plans are built with a forced grid size (no device query). Their reported structure is checked
-against a brute-force restatement of the partition contract in pdattn.h: workgroup w owns the
-kv-head-major page units [U w / W, U (w+1) / W), and a (sequence, kv head) pair is split when
-its units fall into more than one workgroup.
+Plans are built with a forced grid size (no device query). The schedule each plan exports is
+checked against a brute-force restatement of the partition contract in pdattn.h:
+  * chunks of up to P pages of one (sequence, kv head) pair, ordered sequence-major, then by chunk
+    position, with the kv head varying fastest; one unit per page of a chunk;
+  * workgroup w owns the units [U w / W, U (w+1) / W); its segments are the pieces of chunks in
+    its range, in order;
+  * a pair with more than one segment gets consecutive partial slots, its k-th segment (in unit
+    order) writing slot slot0 + k, and one merge-list entry; a pair with one segment writes the
+    final output (slot -1); an empty sequence gets a merge entry with no slots.
 """
 import numpy as np
 import pytest
@@ -12,24 +17,54 @@ import pdattn
 from pdattn import inputs
 
 
-def brute_contributors(indptr, Hkv, W):
-    nnz = int(indptr[-1] - indptr[0])
-    U = Hkv * nnz
-    owner = [0] * U
+def brute_schedule(indptr, last, Hkv, W, P):
+    B = len(indptr) - 1
+    jbase = int(indptr[0])
+    units = []                          # (b, kvh, page index within the sequence)
+    for b in range(B):
+        np_ = int(indptr[b + 1] - indptr[b])
+        for pa in range(0, np_, P):
+            for kvh in range(Hkv):
+                for i in range(pa, min(np_, pa + P)):
+                    units.append((b, kvh, i, pa))
+    U = len(units)
+    segs = []
     for w in range(W):
-        for u in range(U * w // W, U * (w + 1) // W):
-            owner[u] = w
-    split, mx = 0, 1
-    for kvh in range(Hkv):
-        for b in range(len(indptr) - 1):
-            pb, pe = indptr[b] - indptr[0], indptr[b + 1] - indptr[0]
-            if pe == pb:
-                continue
-            ws = {owner[kvh * nnz + j] for j in range(pb, pe)}
-            if len(ws) > 1:
-                split += 1
-            mx = max(mx, len(ws))
-    return U, split, mx
+        u0, u1 = U * w // W, U * (w + 1) // W
+        out = []
+        for u in range(u0, u1):
+            b, kvh, i, pa = units[u]
+            if out and out[-1][0] == b and out[-1][1] == kvh and out[-1][-1] == pa:
+                out[-1][3] += 1
+            else:
+                out.append([b, kvh, u - u0, 1, pa])
+        full = []
+        for b, kvh, qa, npg, pa in out:
+            first = units[u0 + qa][2]
+            np_ = int(indptr[b + 1] - indptr[b])
+            seq_len = (np_ - 1) * 16 + int(last[b])
+            t1 = seq_len if first + npg == np_ else (first + npg) * 16
+            full.append([b, kvh, qa, npg, first * 16, t1, int(indptr[b]) - jbase + first, -1])
+        segs.append(full)
+    # contributors per pair, in unit (= workgroup, segment) order
+    contrib = {}
+    for w, ss in enumerate(segs):
+        for k, sg in enumerate(ss):
+            contrib.setdefault((sg[0], sg[1]), []).append((w, k))
+    merge, slot = [], 0
+    for b in range(B):
+        for kvh in range(Hkv):
+            cs = contrib.get((b, kvh), [])
+            if len(cs) > 1:
+                for k, (w, i) in enumerate(cs):
+                    segs[w][i][7] = slot + k
+                merge.append([b, kvh, slot, len(cs)])
+                slot += len(cs)
+            elif not cs:
+                merge.append([b, kvh, 0, 0])
+    split = sum(1 for cs in contrib.values() if len(cs) > 1)
+    mx = max([len(cs) for cs in contrib.values()] + [1])
+    return U, segs, merge, split, mx
 
 
 CASES = [
@@ -43,26 +78,50 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("lens,Hkv", CASES, ids=[f"{len(c[0])}seq" for c in CASES])
-@pytest.mark.parametrize("W", [1, 3, 7, 64, 256, 1000])
-def test_partition_matches_contract(lens, Hkv, W):
+@pytest.mark.parametrize("lens,Hkv", CASES, ids=[f"{len(c[0])}seq-{c[1]}kv" for c in CASES])
+@pytest.mark.parametrize("W,P", [(1, 16), (3, 16), (7, 5), (64, 16), (256, 16), (256, 8), (1000, 16)])
+def test_schedule_matches_contract(lens, Hkv, W, P):
     bt = inputs.make_batch(lens, Hkv * 4, Hkv, seed=1, fill=False)
     if bt.indptr[-1] == 0:
         pytest.skip("no pages")
-    plan = pdattn.Plan(bt.indptr, bt.last, bt.B, Hkv * 4, Hkv, force_workgroups=W)
+    plan = pdattn.Plan(bt.indptr, bt.last, bt.B, Hkv * 4, Hkv, force_workgroups=W, chunk_pages=P)
     info = plan.info()
-    U, split, mx = brute_contributors(bt.indptr, Hkv, info.workgroups)
+    assert info.chunk_pages == P
+    Wp = info.workgroups
+    assert Wp >= min(W, info.units)              # grows only to respect per-workgroup limits
+    U, segs, merge, split, mx = brute_schedule(bt.indptr, bt.last, Hkv, Wp, P)
+    got_segs, got_merge = plan.schedule()
     assert info.units == U
-    assert 1 <= info.workgroups <= U
-    assert info.workgroups >= min(W, U)          # grows only to respect per-workgroup limits
+    assert got_segs == segs
+    assert got_merge.tolist() == merge
     assert info.split_pairs == split and info.max_contributors == mx
     assert info.pairs == bt.B * Hkv
-    slots = bt.B * Hkv + info.workgroups
+    assert info.segments == sum(len(s) for s in segs)
+    assert info.merge_entries == len(merge)
+    slots = sum(m[3] for m in merge)
     assert info.workspace_bytes >= slots * 4 * 129 * 4
+    # every (page, kv head) unit exactly once
+    seen = set()
+    for ss in got_segs:
+        assert len(ss) <= pdattn.SCHEDULE_SEGMENTS
+        for b, kvh, qa, npg, t0, t1, jpos, slot in ss:
+            for i in range(npg):
+                key = (kvh, jpos + i)
+                assert key not in seen
+                seen.add(key)
+    assert len(seen) == U
+
+
+def test_every_workgroup_mixes_kv_heads():
+    """One long sequence: every workgroup's range covers several kv heads (the order's purpose)."""
+    bt = inputs.make_batch([32768], 32, 8, seed=1, fill=False)
+    plan = pdattn.Plan(bt.indptr, bt.last, bt.B, 32, 8, force_workgroups=256, chunk_pages=16)
+    segs, _ = plan.schedule()
+    assert all(len({s[1] for s in ss}) >= 4 for ss in segs)
 
 
 def test_many_tiny_sequences_grow_the_grid():
-    """More sequences per workgroup than descriptor slots: the planner doubles the grid."""
+    """More segments per workgroup than descriptor slots: the planner doubles the grid."""
     lens = [16] * 4096
     bt = inputs.make_batch(lens, 32, 8, seed=2, fill=False)
     plan = pdattn.Plan(bt.indptr, bt.last, bt.B, 32, 8, force_workgroups=256)
@@ -73,3 +132,11 @@ def test_all_empty_batch():
     plan = pdattn.Plan([0, 0, 0], [0, 0], 2, 8, 2, force_workgroups=5)
     info = plan.info()
     assert info.units == 0 and info.split_pairs == 0
+    _, merge = plan.schedule()
+    assert merge.tolist() == [[0, 0, 0, 0], [0, 1, 0, 0], [1, 0, 0, 0], [1, 1, 0, 0]]
+
+
+def test_rejects_bad_chunk_pages():
+    bt = inputs.make_batch([100], 8, 2, seed=1, fill=False)
+    with pytest.raises(pdattn.PdattnError):
+        pdattn.Plan(bt.indptr, bt.last, bt.B, 8, 2, force_workgroups=4, chunk_pages=-1)
