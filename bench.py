@@ -138,7 +138,7 @@ def uniform_runner(bt, t, stream):
 
 ROT_BYTES = 1 << 30
 COPY_BYTES = 256 << 20
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_streamk_1x32k_traffic.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_balanced_1x32k_traffic.md")
 
 
 def ceiling_gbs(timer, steps):

@@ -536,7 +536,7 @@ struct BalSmem {
     float m[NS][G];
     float l[NS][G];
     float o[NS][G][OP];
-    float alpha[NS][G];       // exp(m_src - M) per source and head
+    float alpha[G][NS];       // exp(m_src - M) per head and source
     float rinv[G];            // 1 / L
     float lse[G];
 };
@@ -552,16 +552,34 @@ __device__ __forceinline__ void reset_state(WaveState<C>& st) {
     }
 }
 
+// Reduction (max or sum) over the lanes that agree modulo G (G in 1, 2, 4, 8), leaving the result
+// in every one of them, in the VALU: quad permutations for lane distances 1 and 2, row
+// rotations by 8 and 4 within a 16-lane row (after which every lane of the row holds the result
+// of its class), and the row-pair swaps across rows.
+template <int G, bool MAX>
+__device__ __forceinline__ float class_reduce(float v) {
+    auto op = [](float x, float y) { return MAX ? fmaxf(x, y) : x + y; };
+    if constexpr (G == 1) v = op(v, dpp<0xB1>(v));   // quad_perm [1,0,3,2]
+    if constexpr (G <= 2) v = op(v, dpp<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = op(v, dpp<0x128>(v));                        // row_ror:8
+    if constexpr (G <= 4) v = op(v, dpp<0x124>(v));  // row_ror:4
+    float x, y;
+    row_pair<false>(v, x, y);
+    row_pair<true>(op(x, y), x, y);
+    return op(x, y);
+}
+
 // End of a segment. Every row group of every wave is one source state (max, sum, output slice);
-// all of them go to LDS unmerged, one wave turns the per-source maxima into weights, and every
-// thread forms its outputs as one weighted sum over the sources, in source order. Writes the G
+// all of them go to LDS unmerged, one wave turns the per-source maxima into weights, and each
+// thread forms four outputs as one weighted sum over the sources, in source order. Writes the G
 // rows as the final fp16 out / lse (slot < 0) or as partial slot `slot` (normalized o, lse).
 template <class C>
 __device__ __forceinline__ void flush_segment(BalSmem<C::G, C::NW * C::RPI>& sm, WaveState<C>& st,
                                               KArgPtr a, size_t row0, int slot) {
-    constexpr int G = C::G, NT = C::NT, LPR = C::LPR, NS = C::NW * C::RPI;
+    constexpr int G = C::G, LPR = C::LPR, NS = C::NW * C::RPI;
     // one wave computes the source weights: lane = s * G + h covers sources s + j * SL, j < J
     constexpr int SL = 64 / G, J = (NS + SL - 1) / SL;
+    static_assert(NS % 4 == 0 && G * 32 <= C::NT, "float4 passes");
     const int tid = threadIdx.x, lane = tid & 63, c = lane % LPR;
     const int src = (tid >> 6) * C::RPI + lane / LPR;
 #pragma unroll
@@ -590,38 +608,53 @@ __device__ __forceinline__ void flush_segment(BalSmem<C::G, C::NW * C::RPI>& sm,
             mv[j] = s < NS ? sm.m[s][h] : -INFINITY;
             M = fmaxf(M, mv[j]);
         }
-#pragma unroll
-        for (int off = G; off < 64; off <<= 1) M = fmaxf(M, __shfl_xor(M, off));
+        M = class_reduce<G, true>(M);
         float L = 0.f;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const int s = s0 + j * SL;
             const float al = (mv[j] == -INFINITY) ? 0.f : fast_exp2(mv[j] - M);
             if (s < NS) {
-                sm.alpha[s][h] = al;
+                sm.alpha[h][s] = al;
                 L = fmaf(al, sm.l[s][h], L);
             }
         }
-#pragma unroll
-        for (int off = G; off < 64; off <<= 1) L += __shfl_xor(L, off);
+        L = class_reduce<G, false>(L);
         if (tid < G) {
             sm.rinv[h] = L > 0.f ? 1.f / L : 0.f;
             sm.lse[h] = L > 0.f ? (M + fast_log2(L)) * kLn2 : -INFINITY;
         }
     }
     __syncthreads();
-    for (int idx = tid; idx < G * kHeadDim; idx += NT) {
-        const int h = idx / kHeadDim, d = idx % kHeadDim;
-        float O = 0.f;
+    if (tid < G * 32) {
+        const int h = tid / 32, d0 = 4 * (tid % 32);
+        float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int s = 0; s < NS; ++s) O = fmaf(sm.alpha[s][h], sm.o[s][h][d], O);
-        const float val = O * sm.rinv[h];
+        for (int s4 = 0; s4 < NS; s4 += 4) {
+            const float4 al = *reinterpret_cast<const float4*>(&sm.alpha[h][s4]);
+            const float alv[4] = {al.x, al.y, al.z, al.w};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float4 ov = *reinterpret_cast<const float4*>(&sm.o[s4 + u][h][d0]);
+                O.x = fmaf(alv[u], ov.x, O.x);
+                O.y = fmaf(alv[u], ov.y, O.y);
+                O.z = fmaf(alv[u], ov.z, O.z);
+                O.w = fmaf(alv[u], ov.w, O.w);
+            }
+        }
+        const float ri = sm.rinv[h];
+        O.x *= ri;
+        O.y *= ri;
+        O.z *= ri;
+        O.w *= ri;
         if (slot < 0) {
-            a->out[(row0 + h) * kHeadDim + d] = (_Float16)val;
-            if (d == 0) a->lse[row0 + h] = sm.lse[h];
+            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+            const h4 hv = {(_Float16)O.x, (_Float16)O.y, (_Float16)O.z, (_Float16)O.w};
+            *reinterpret_cast<h4*>(a->out + (row0 + h) * kHeadDim + d0) = hv;
+            if (d0 == 0) a->lse[row0 + h] = sm.lse[h];
         } else {
-            a->part_o[((size_t)slot * G + h) * kHeadDim + d] = val;
-            if (d == 0) a->part_lse[(size_t)slot * G + h] = sm.lse[h];
+            *reinterpret_cast<float4*>(a->part_o + ((size_t)slot * G + h) * kHeadDim + d0) = O;
+            if (d0 == 0) a->part_lse[(size_t)slot * G + h] = sm.lse[h];
         }
     }
     __syncthreads();   // sm is reused by the next segment
@@ -638,18 +671,17 @@ __global__ __launch_bounds__(C::NT) void decode_balanced_kernel(BalArgs a) {
     constexpr int G = C::G, NW = C::NW, NT = C::NT, NBUF = C::NBUF, LPR = C::LPR;
     __shared__ BalSmem<G, NW * C::RPI> sm;
     __shared__ int pg[kRangeMax];
-    __shared__ int sd[kSegMax * kSegInts];
     __shared__ u32x4 qs[kSegMax][G * kHeadDim / 8];
     // the wave index is made wave-uniform explicitly: everything the page ring derives from it
     // (per-wave page counts, page ids, buffer resources) must live in scalar registers
     const int w = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane / LPR, c = lane % LPR;
-    // Segment fields are read from LDS and made wave-uniform: global (vector) loads of them would
-    // count against the same wait counter as the ring's page loads, and a non-uniform value in a
-    // buffer resource would turn every page load into a loop over lanes.
+    // Segment fields are staged in LDS and read back wave-uniform: global (vector) loads of them
+    // would count against the same wait counter as the ring's page loads, and a non-uniform value
+    // in a buffer resource would turn every page load into a loop over lanes.
+    __shared__ int sd[kSegMax * kSegInts];
     auto fld = [&](int si, int f) { return __builtin_amdgcn_readfirstlane(sd[si * kSegInts + f]); };
-
     const int32_t* desc = kargs()->desc + (size_t)w * kBalDescInts;
     const int nseg = __builtin_amdgcn_readfirstlane(desc[0]);
     if (nseg <= 0) return;   // uniform: the planner gives every workgroup at least one segment
