@@ -39,7 +39,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", default="", choices=["", "32k", "64x1k", "cascade"],
+    ap.add_argument("--only", default="", choices=["", "32k", "64x1k", "cascade", "append"],
                     help="run one workload only (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only torch copies of COPY_BYTES (known-size traffic for counter runs)")
@@ -285,6 +285,35 @@ def cascade_workload(timer, args):
     return out
 
 
+def append_workload(timer, args):
+    """Paged KV append: all 32768 tokens of one sequence (the 1x32K caches: 2 x 134 MB read and
+    written), and one decode step (one token for each of 64 sequences of 1K)."""
+    import torch
+    import pdattn
+    s = timer.stream
+    d = torch.device("cuda:0")
+    out = {}
+    for tag, lens, full in [("prefill_1x32K", [32768], True), ("decode_step_64x1K", [1024] * 64, False)]:
+        bt, t = make_device_batch(lens, 32, 8, seed=13)
+        if full:
+            bidx = torch.zeros(lens[0], dtype=torch.int32, device=d)
+            pos = torch.arange(lens[0], dtype=torch.int32, device=d)
+        else:
+            bidx = torch.arange(bt.B, dtype=torch.int32, device=d)
+            pos = torch.tensor([L - 1 for L in lens], dtype=torch.int32, device=d)
+        n = bidx.numel()
+        kn = torch.randn(n, 8, 128, device=d, dtype=torch.float32).half()
+        vn = torch.randn(n, 8, 128, device=d, dtype=torch.float32).half()
+        fn = lambda: pdattn.append_kv(kn, vn, t["k"], t["v"], t["indptr"], t["indices"], bidx, pos,  # noqa: E731
+                                      bt.B, 8, stream=s)
+        ms = statistics.median(timer.run([fn], args.steps, args.warmup)[0])
+        nbytes = 2 * 2 * n * 8 * 128 * 2           # K and V rows, read and written
+        out[tag] = {"tokens": n, "us_per_step": round(ms * 1e3, 2),
+                    "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes}
+        del t, kn, vn
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -302,6 +331,9 @@ def main():
     timer = Timer()
     if args.only == "cascade":
         print(json.dumps({"cascade_64x(8192+512)": cascade_workload(timer, args)}))
+        return
+    if args.only == "append":
+        print(json.dumps({"append_kv": append_workload(timer, args)}))
         return
     lens = [1024] * 64 if args.only == "64x1k" else [32768]
     name = ("paged GQA decode B=64 L=1024 (metric's 64x1K)" if args.only == "64x1k"
@@ -345,6 +377,7 @@ def main():
                         "kernel_frac_of_ceiling": round(a2 / ceil, 4),
                         "workgroups": h2["workgroups"], "algorithmic_bytes": h2["bytes"]}
         sec["cascade_64x(8192+512)"] = cascade_workload(timer, args)
+        sec["append_kv"] = append_workload(timer, args)
         result["secondary"] = sec
     if not args.no_cpu_baseline and not args.only:
         result["cpu_baseline"] = cpu_baseline([32768], 32, 8, seed=11)

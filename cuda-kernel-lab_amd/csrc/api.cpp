@@ -801,6 +801,36 @@ void pdattn_cascade_plan_destroy(pdattn_cascade_plan* cp) {
     delete cp;
 }
 
+int pdattn_append_kv(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                     const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* batch_idx,
+                     const int32_t* positions, int n, int B, int Hkv, int32_t* n_invalid,
+                     void* stream) {
+    if (n < 0 || B < 0 || Hkv <= 0)
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "n=%d B=%d Hkv=%d", n, B, Hkv);
+    if (n == 0) return PDATTN_OK;
+    if (!k_new || !v_new || !k_cache || !v_cache || !kv_indptr || !kv_indices || !batch_idx || !positions)
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "null device pointer");
+    if (!aligned16(k_new) || !aligned16(v_new) || !aligned16(k_cache) || !aligned16(v_cache))
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "K/V inputs and caches must be 16-byte aligned");
+    DeviceFacts f;
+    if (int st = device_facts(&f)) return st;
+    AppendArgs a;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.kv_indptr = kv_indptr;
+    a.kv_indices = kv_indices;
+    a.batch_idx = batch_idx;
+    a.positions = positions;
+    a.n_invalid = n_invalid;
+    a.n = n;
+    a.B = B;
+    a.Hkv = Hkv;
+    PD_HIP(launch_append_kv(a, f.cus, static_cast<hipStream_t>(stream)));
+    return PDATTN_OK;
+}
+
 int pdattn_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream) {
     if (!buf || !sink || bytes % 16) return fail(PDATTN_ERR_INVALID_ARGUMENT, "buf/sink null or bytes %% 16 != 0");
     if (bytes == 0) return PDATTN_OK;

@@ -68,6 +68,20 @@ struct MergeArgs {
     int Hq, G, n_extra;
 };
 
+// Paged KV append: token t (of n) of sequence batch_idx[t] at position positions[t].
+struct AppendArgs {
+    const void*     k_new;        // [n, Hkv, 128] fp16
+    const void*     v_new;
+    void*           k_cache;      // [num_pages, 16, Hkv, 128] fp16
+    void*           v_cache;
+    const int32_t*  kv_indptr;
+    const int32_t*  kv_indices;
+    const int32_t*  batch_idx;
+    const int32_t*  positions;
+    int32_t*        n_invalid;    // optional: tokens outside their sequence's pages
+    int n, B, Hkv;
+};
+
 // Arguments of the MFMA shared-prefix kernel.
 struct PrefixArgs {
     const _Float16* q;
@@ -88,6 +102,7 @@ hipError_t launch_decode_balanced(const BalArgs& a, int G, hipStream_t s);
 hipError_t launch_merge_split(const MergeArgs& a, int n_entries, hipStream_t s);
 hipError_t launch_fill_i32(int32_t* p, int32_t value, size_t n, hipStream_t s);
 hipError_t launch_cascade_prefix(const PrefixArgs& a, int G, int qtiles, hipStream_t s);
+hipError_t launch_append_kv(const AppendArgs& a, int cus, hipStream_t s);
 hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, int grid, hipStream_t s);
 hipError_t launch_flush(void* buf, size_t bytes, int grid, hipStream_t s);
 

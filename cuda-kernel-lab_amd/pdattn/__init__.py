@@ -42,6 +42,7 @@ EXPORTS = [
     "pdattn_shared_prefix_pages", "pdattn_cascade_prefix",
     "pdattn_cascade_plan_create", "pdattn_cascade_plan_get_info", "pdattn_cascade_decode",
     "pdattn_cascade_plan_destroy",
+    "pdattn_append_kv",
     "pdattn_stream_read", "pdattn_flush_cache", "pdattn_get_device_info",
 ]
 
@@ -148,6 +149,7 @@ def lib():
         "pdattn_cascade_plan_get_info": ([P, ctypes.POINTER(CascadeInfo)], I),
         "pdattn_cascade_decode": ([P, P, P, ctypes.POINTER(Workspace), P], I),
         "pdattn_cascade_plan_destroy": ([P], None),
+        "pdattn_append_kv": ([P, P, P, P, P, P, P, P, I, I, I, P, P], I),
         "pdattn_stream_read": ([P, S, P, P], I),
         "pdattn_flush_cache": ([P, S, P], I),
         "pdattn_get_device_info": ([ctypes.POINTER(DeviceInfo)], I),
@@ -311,6 +313,19 @@ class Plan:
             self.close()
         except Exception:
             pass
+
+
+# ---- paged KV append ---------------------------------------------------------------------------
+
+def append_kv(k_new, v_new, k_cache, v_cache, kv_indptr, kv_indices, batch_idx, positions,
+              B: int, Hkv: int, n_invalid=None, stream=None):
+    """pdattn_append_kv: write token t's K/V rows at position positions[t] of sequence
+    batch_idx[t] (the page table already covers the appended tokens)."""
+    n = int(batch_idx.shape[0]) if hasattr(batch_idx, "shape") else len(batch_idx)
+    _check(lib().pdattn_append_kv(ptr(k_new), ptr(v_new), ptr(k_cache), ptr(v_cache), ptr(kv_indptr),
+                                  ptr(kv_indices), ptr(batch_idx), ptr(positions), n, B, Hkv,
+                                  ptr(n_invalid) if n_invalid is not None else None,
+                                  stream_ptr(stream)), "pdattn_append_kv")
 
 
 # ---- cascade ---------------------------------------------------------------------------------

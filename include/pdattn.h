@@ -225,6 +225,22 @@ int pdattn_cascade_decode(pdattn_cascade_plan* plan, void* out, float* lse, pdat
                           void* stream);
 void pdattn_cascade_plan_destroy(pdattn_cascade_plan* plan);
 
+/* ---- paged KV append ---------------------------------------------------------------------- */
+
+/* Write n new tokens' K and V rows ([n, Hkv, 128] fp16 each) into the paged caches. The page
+ * table already describes the caches after the append (the caller has allocated the pages and
+ * set kv_indptr / kv_last_page_len, as with FlashInfer's append_paged_kv_cache): token t, at
+ * position positions[t] of sequence batch_idx[t], goes to page kv_indices[kv_indptr[b] +
+ * pos / 16], slot pos % 16, for every kv head. Layout as in the decode path
+ * (01_decode_attention.cu:5-9, 112). A token whose sequence or position is out of range is
+ * skipped and counted in *n_invalid (device int32, optional; the caller zeroes it). No
+ * counterpart in the reference, which builds its caches on the host (01:402-431); this is the
+ * write side of the same page format. */
+int pdattn_append_kv(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                     const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* batch_idx,
+                     const int32_t* positions, int n, int B, int Hkv, int32_t* n_invalid,
+                     void* stream);
+
 /* ---- measurement helpers ------------------------------------------------------------------ */
 
 /* Streams `bytes` (a multiple of 16) with 16-byte loads and folds them into one word, written

@@ -175,3 +175,44 @@ def plan_chunks_ref(resident_blocks: int, B: int, Hkv: int, max_len: int, force_
     lib().oracle_plan_chunks_ref(resident_blocks, B, Hkv, max_len, force_chunks,
                                  ctypes.byref(nc), ctypes.byref(ct))
     return nc.value, ct.value
+
+
+APPEND_FAULTS = ("none", "slot_kvh_transpose", "page_off_by_one", "position_minus_one")
+
+
+def append_kv(k_cache, v_cache, k_new, v_new, batch_idx, positions, indptr, indices,
+              fault: str = "none"):
+    """Paged KV append, restated on the host: token t, at position p of sequence b, is written to
+    page indices[indptr[b] + p // 16], slot p % 16, for every kv head -- the page addressing of
+    01_decode_attention.cu:112 used for writes (FlashInfer's append convention: the page table
+    already covers the appended tokens). Tokens whose sequence or position is out of range are
+    skipped and counted. Caches are [num_pages, 16, Hkv, 128] (any 2-byte dtype), new rows
+    [n, Hkv, 128]. `fault` plants a mistake for the tests that pin this function.
+
+    Returns (k_cache', v_cache', n_invalid)."""
+    kc, vc = np.array(k_cache, copy=True), np.array(v_cache, copy=True)
+    indptr, indices = np.asarray(indptr), np.asarray(indices)
+    B = len(indptr) - 1
+    bad = 0
+    for t in range(len(batch_idx)):
+        b, p = int(batch_idx[t]), int(positions[t])
+        if fault == "position_minus_one":
+            p -= 1
+        if b < 0 or b >= B or p < 0 or p >= (indptr[b + 1] - indptr[b]) * PAGE:
+            bad += 1
+            continue
+        j = indptr[b] + p // PAGE + (1 if fault == "page_off_by_one" else 0)
+        j = min(j, len(indices) - 1)
+        page, slot = int(indices[j]), p % PAGE
+        if fault == "slot_kvh_transpose":
+            # rows laid out [kvh][slot] instead of [slot][kvh]
+            flat_k, flat_v = kc[page].reshape(-1, HEAD_DIM), vc[page].reshape(-1, HEAD_DIM)
+            Hkv = kc.shape[2]
+            for h in range(Hkv):
+                flat_k[(h * PAGE + slot) % (PAGE * Hkv)] = k_new[t, h]
+                flat_v[(h * PAGE + slot) % (PAGE * Hkv)] = v_new[t, h]
+            continue
+        kc[page, slot] = k_new[t]
+        vc[page, slot] = v_new[t]
+    return kc, vc, bad
+
