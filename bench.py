@@ -39,7 +39,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", default="", choices=["", "32k", "64x1k", "cascade", "append"],
+    ap.add_argument("--only", default="", choices=["", "32k", "64x1k", "cascade", "append", "graph"],
                     help="run one workload only (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only torch copies of COPY_BYTES (known-size traffic for counter runs)")
@@ -314,6 +314,46 @@ def append_workload(timer, args):
     return out
 
 
+def graph_workload(timer, args):
+    """A whole step captured as one HIP graph vs the same launches made eagerly (same cold-cache
+    method): the 1x32K balanced step (decode + merge) and the cascade step (prefix + suffix +
+    merge)."""
+    import torch
+    import pdattn
+    s = timer.stream
+    out = {}
+    bt, t = make_device_batch([32768], 32, 8, seed=11)
+    fn, plan, ws = streamk_runner(bt, t, s)
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        plan.run(t["q"], t["k"], t["v"], t["indptr"], t["indices"], t["last"], t["out"], t["lse"],
+                 ws, ws.numel(), stream=torch.cuda.current_stream())
+    we, wg = timer.run([fn, g.replay], args.steps, args.warmup, rounds=3)
+    out["1x32K"] = {"eager_us": round(statistics.median(we) * 1e3, 2),
+                    "graph_us": round(statistics.median(wg) * 1e3, 2)}
+    del t, ws, g
+    bt3, t3 = make_device_batch(None, 32, 8, seed=21, shared_prefix=8192, suffix=[512] * 64)
+    base = pdattn.make_params(t3["q"], t3["k"], t3["v"], t3["indptr"], t3["indices"], t3["last"],
+                              bt3.B, 32, 8)
+    cp = pdattn.CascadePlan(base, bt3.indptr, bt3.indices, bt3.lens, t3["indices"])
+    cws = pdattn.Workspace()
+    fc = lambda: cp.decode(t3["out"], t3["lse"], cws, s)  # noqa: E731
+    fc()
+    torch.cuda.synchronize()
+    g3 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g3):
+        cp.decode(t3["out"], t3["lse"], cws, torch.cuda.current_stream())
+    we, wg = timer.run([fc, g3.replay], args.steps, args.warmup, rounds=3)
+    out["cascade_64x(8192+512)"] = {"eager_us": round(statistics.median(we) * 1e3, 2),
+                                    "graph_us": round(statistics.median(wg) * 1e3, 2)}
+    cp.close()
+    pdattn.workspace_release(cws)
+    del t3, g3
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -334,6 +374,9 @@ def main():
         return
     if args.only == "append":
         print(json.dumps({"append_kv": append_workload(timer, args)}))
+        return
+    if args.only == "graph":
+        print(json.dumps({"hip_graph": graph_workload(timer, args)}))
         return
     lens = [1024] * 64 if args.only == "64x1k" else [32768]
     name = ("paged GQA decode B=64 L=1024 (metric's 64x1K)" if args.only == "64x1k"
@@ -378,6 +421,7 @@ def main():
                         "workgroups": h2["workgroups"], "algorithmic_bytes": h2["bytes"]}
         sec["cascade_64x(8192+512)"] = cascade_workload(timer, args)
         sec["append_kv"] = append_workload(timer, args)
+        sec["hip_graph"] = graph_workload(timer, args)
         result["secondary"] = sec
     if not args.no_cpu_baseline and not args.only:
         result["cpu_baseline"] = cpu_baseline([32768], 32, 8, seed=11)
