@@ -354,6 +354,25 @@ def graph_workload(timer, args):
     return out
 
 
+def op_workload(timer, args):
+    """torch.ops.pdattn.paged_decode (plan cached by table contents) vs the direct plan call, 1x32K."""
+    import torch
+    import pdattn
+    import pdattn.torch_ops  # noqa: F401
+    s = timer.stream
+    bt, t = make_device_batch([32768], 32, 8, seed=11)
+    fn, plan, ws = streamk_runner(bt, t, s)
+    iph = torch.from_numpy(bt.indptr.astype("int32"))
+    lah = torch.from_numpy(bt.last.astype("int32"))
+    sc = float(1.0 / 128 ** 0.5)
+    op = lambda: torch.ops.pdattn.paged_decode(t["q"], t["k"], t["v"], t["indptr"], t["indices"],  # noqa: E731
+                                               t["last"], iph, lah, sc)
+    wd, wo = timer.run([fn, op], args.steps, args.warmup, rounds=3)
+    del t, ws
+    return {"1x32K": {"direct_us": round(statistics.median(wd) * 1e3, 2),
+                      "op_us": round(statistics.median(wo) * 1e3, 2)}}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -422,6 +441,7 @@ def main():
         sec["cascade_64x(8192+512)"] = cascade_workload(timer, args)
         sec["append_kv"] = append_workload(timer, args)
         sec["hip_graph"] = graph_workload(timer, args)
+        sec["torch_op"] = op_workload(timer, args)
         result["secondary"] = sec
     if not args.no_cpu_baseline and not args.only:
         result["cpu_baseline"] = cpu_baseline([32768], 32, 8, seed=11)
