@@ -39,7 +39,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", default="", choices=["", "32k", "64x1k", "cascade", "append", "graph"],
+    ap.add_argument("--only", default="", choices=["", "32k", "64x1k", "cascade", "append", "graph",
+                                                   "tree"],
                     help="run one workload only (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only torch copies of COPY_BYTES (known-size traffic for counter runs)")
@@ -373,6 +374,49 @@ def op_workload(timer, args):
                       "op_us": round(statistics.median(wo) * 1e3, 2)}}
 
 
+def tree_workload(timer, args):
+    """Multi-level cascade: 64 requests = a 2048-token system prompt shared by all, then 8
+    documents of 4096 tokens each shared by 8 requests, then 256 private tokens each. Non-shared
+    decode vs the single-level cascade (system prompt only) vs the tree cascade."""
+    import torch
+    import pdattn
+    from pdattn import inputs
+    s = timer.stream
+    nodes = [((0,), 2048)] + [((0, g), 4096) for g in range(1, 9)]
+    seqs = [((0, g), 256) for g in range(1, 9) for _ in range(8)]
+    bt = inputs.make_prefix_tree_batch(nodes, seqs, 32, 8, seed=23, fill=False)
+    d = torch.device("cuda:0")
+    g = torch.Generator(device=d)
+    g.manual_seed(23)
+    t = dict(q=torch.randn(bt.B, 32, 128, generator=g, device=d, dtype=torch.float32).half(),
+             k=torch.randn(bt.num_pages, 16, 8, 128, generator=g, device=d, dtype=torch.float32).half(),
+             v=torch.randn(bt.num_pages, 16, 8, 128, generator=g, device=d, dtype=torch.float32).half(),
+             indptr=torch.from_numpy(bt.indptr).to(d), indices=torch.from_numpy(bt.indices).to(d),
+             last=torch.from_numpy(bt.last).to(d),
+             out=torch.empty(bt.B, 32, 128, dtype=torch.float16, device=d),
+             lse=torch.empty(bt.B, 32, dtype=torch.float32, device=d))
+    fn, plan, ws = streamk_runner(bt, t, s)
+    base = pdattn.make_params(t["q"], t["k"], t["v"], t["indptr"], t["indices"], t["last"], bt.B, 32, 8)
+    plans, fns = [], [fn]
+    for tree in (False, True):
+        cp = pdattn.CascadePlan(base, bt.indptr, bt.indices, bt.lens, t["indices"], 256, tree)
+        cws = pdattn.Workspace()
+        cp.decode(t["out"], t["lse"], cws, s)
+        plans.append((cp, cws))
+        fns.append(lambda cp=cp, cws=cws: cp.decode(t["out"], t["lse"], cws, s))
+    wn, w1, wt = timer.run(fns, args.steps, args.warmup, rounds=3)
+    mn, m1, mt = (statistics.median(w) * 1e3 for w in (wn, w1, wt))
+    info = plans[1][0].info()
+    for cp, cws in plans:
+        cp.close()
+        pdattn.workspace_release(cws)
+    del t, ws
+    return {"requests": 64, "non_shared_us": round(mn, 2), "single_level_us": round(m1, 2),
+            "tree_us": round(mt, 2), "tree_speedup_vs_non_shared": round(mn / mt, 2),
+            "tree_speedup_vs_single_level": round(m1 / mt, 2), "tree_nodes": info.nodes,
+            "tree_levels": info.levels}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -396,6 +440,9 @@ def main():
         return
     if args.only == "graph":
         print(json.dumps({"hip_graph": graph_workload(timer, args)}))
+        return
+    if args.only == "tree":
+        print(json.dumps({"cascade_tree": tree_workload(timer, args)}))
         return
     lens = [1024] * 64 if args.only == "64x1k" else [32768]
     name = ("paged GQA decode B=64 L=1024 (metric's 64x1K)" if args.only == "64x1k"
@@ -442,6 +489,7 @@ def main():
         sec["append_kv"] = append_workload(timer, args)
         sec["hip_graph"] = graph_workload(timer, args)
         sec["torch_op"] = op_workload(timer, args)
+        sec["cascade_tree"] = tree_workload(timer, args)
         result["secondary"] = sec
     if not args.no_cpu_baseline and not args.only:
         result["cpu_baseline"] = cpu_baseline([32768], 32, 8, seed=11)

@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -178,16 +179,30 @@ struct pdattn_plan {
     const void* uploaded_to = nullptr;
 };
 
+// One node of a shared-prefix tree: the ns sequences seqs[seq_off ..] all hold the same physical
+// pages at positions [p0, p1) of their page lists (page-table positions jpos .. of the first
+// member), and each keeps at least one page of its own after p1.
+struct CascadeNode {
+    int p0 = 0, p1 = 0, jpos = 0, depth = 0;
+    int seq_off = 0, ns = 0;
+    int ctok = 0, nchunks = 0, col0 = 0, qgroups = 0;
+};
+
 struct pdattn_cascade_plan {
     int use = 0;
-    int P = 0, Lp = 0;                 // shared pages / tokens
-    int cpre = 0, ctok = 0, qgroups = 0;
+    int Lp = 0;                        // tokens of the first node (the batch-wide prefix, if any)
+    int levels = 0;                    // depth of the node tree
+    int n_extra = 0;                   // prefix partial columns per row
+    std::vector<int> level_items;      // items (workgroups per kv head) of each depth's launch
+    int n_items = 0;
     pdattn_decode_params base{};
-    const int32_t* d_prefix_pages = nullptr;
+    const int32_t* d_indices = nullptr;
+    std::vector<CascadeNode> nodes;
     pdattn_plan sk;                    // balanced plan of the suffix (or of the whole batch)
-    std::vector<int32_t> tbl;          // suffix indptr [B+1] then suffix indices [nnz_s]
+    std::vector<int32_t> blob;         // suffix indptr [B+1], suffix indices, node members
+    int n_suffix_idx = 0, n_seqs = 0;
     void* pinned = nullptr;
-    size_t off_ppo = 0, off_pplse = 0, off_tbl = 0, off_sk = 0, ws_bytes = 0;
+    size_t off_ppo = 0, off_pplse = 0, off_blob = 0, off_sk = 0, ws_bytes = 0;
     const void* uploaded_to = nullptr;
 };
 
@@ -410,6 +425,200 @@ int run_plan(const pdattn_plan* pl, const void* q, const void* k, const void* v,
         m.n_extra = n_extra;
         PD_HIP(launch_merge_split(m, pl->n_entries, s));
     }
+    return PDATTN_OK;
+}
+
+
+// Nodes of the shared-prefix structure of a batch and the first suffix page of every sequence.
+// tree = false: the reference's rule (plan_cascade, 01_decode_attention.cu:656-701): one node,
+// the longest prefix every sequence shares (shared_prefix_pages), used if it holds at least
+// min_prefix tokens. tree = true: a prefix tree. A group of sequences that share the page at
+// position p0 extends its node while every member holds the same page and keeps a page of its
+// own after it; a node of at least min_prefix tokens is kept, and the group splits by the page
+// that follows, each subgroup of two or more sequences descending. A group whose shared run is
+// shorter than min_prefix stops there (its pages are decoded with each member's suffix).
+void build_cascade_nodes(const int32_t* indptr, const int32_t* indices, int B, int min_prefix,
+                         bool tree, std::vector<CascadeNode>& nodes, std::vector<int32_t>& seqs,
+                         std::vector<int>& suffix_start) {
+    suffix_start.assign(std::max(1, B), 0);
+    auto np = [&](int b) { return indptr[b + 1] - indptr[b]; };
+    auto page = [&](int b, int p) { return indices[indptr[b] + p]; };
+    if (!tree) {
+        const int P = B > 0 ? pdattn_shared_prefix_pages(indptr, indices, B) : 0;
+        if (P > 0 && P * kPage >= min_prefix) {
+            CascadeNode n;
+            n.p0 = 0;
+            n.p1 = P;
+            n.jpos = indptr[0];
+            n.seq_off = 0;
+            n.ns = B;
+            nodes.push_back(n);
+            for (int b = 0; b < B; ++b) seqs.push_back(b);
+            for (int b = 0; b < B; ++b) suffix_start[b] = P;
+        }
+        return;
+    }
+    struct Work { std::vector<int> S; int p0, depth; };
+    std::vector<Work> stack;
+    // the root groups: sequences with two or more pages, by their first page
+    std::map<int, std::vector<int>> roots;
+    for (int b = 0; b < B; ++b)
+        if (np(b) >= 2) roots[page(b, 0)].push_back(b);
+    for (auto& kv : roots)
+        if (kv.second.size() >= 2) stack.push_back({kv.second, 0, 0});
+    while (!stack.empty()) {
+        Work wk = std::move(stack.back());
+        stack.pop_back();
+        int p = wk.p0;
+        for (;;) {
+            bool ok = true;
+            for (int b : wk.S)
+                if (p >= np(b) - 1 || page(b, p) != page(wk.S[0], p)) { ok = false; break; }
+            if (!ok) break;
+            ++p;
+        }
+        if ((p - wk.p0) * kPage < min_prefix || p == wk.p0) continue;   // members keep start p0
+        CascadeNode n;
+        n.p0 = wk.p0;
+        n.p1 = p;
+        n.jpos = indptr[wk.S[0]] + wk.p0;
+        n.depth = wk.depth;
+        n.seq_off = (int)seqs.size();
+        n.ns = (int)wk.S.size();
+        nodes.push_back(n);
+        seqs.insert(seqs.end(), wk.S.begin(), wk.S.end());
+        std::map<int, std::vector<int>> sub;
+        for (int b : wk.S) {
+            suffix_start[b] = p;
+            if (p < np(b) - 1) sub[page(b, p)].push_back(b);
+        }
+        for (auto& kv : sub)
+            if (kv.second.size() >= 2) stack.push_back({kv.second, p, wk.depth + 1});
+    }
+}
+
+int cascade_plan_create(const pdattn_decode_params* base, const int32_t* h_indptr,
+                        const int32_t* h_indices, const int32_t* h_lens, const int32_t* d_indices,
+                        int min_prefix, bool tree, pdattn_cascade_plan** plan) {
+    if (!plan) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null plan output");
+    *plan = nullptr;
+    if (!base) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null base params");
+    int G = 0;
+    if (int st = check_heads(base->Hq, base->Hkv, &G)) return st;
+    const int B = base->B;
+    if (B < 0) return fail(PDATTN_ERR_INVALID_ARGUMENT, "B=%d is negative", B);
+    if (base->kv_start != 0) return fail(PDATTN_ERR_INVALID_ARGUMENT, "cascade base must have kv_start = 0");
+    if (B > 0 && (!h_indptr || !h_indices || !h_lens || !d_indices))
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "null host table / lens / device indices");
+    if (B > 0 && (!base->q || !base->k_cache || !base->v_cache || !base->kv_indptr || !base->kv_indices ||
+                  !base->kv_last_page_len))
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "null device pointer in base params");
+    if (!std::isfinite(base->sm_scale)) return fail(PDATTN_ERR_INVALID_ARGUMENT, "sm_scale is not finite");
+    // last-page lengths from the sequence lengths (ceil(L/16) pages each)
+    std::vector<int32_t> last(std::max(1, B), 0);
+    for (int b = 0; b < B; ++b) {
+        const int np = h_indptr[b + 1] - h_indptr[b];
+        if (np < 0) return fail(PDATTN_ERR_PAGE_TABLE, "indptr not monotone at %d", b);
+        if (h_lens[b] < 0 || (h_lens[b] + kPage - 1) / kPage != np)
+            return fail(PDATTN_ERR_PAGE_TABLE, "lens[%d]=%d does not match its %d pages", b, h_lens[b], np);
+        last[b] = np > 0 ? h_lens[b] - (np - 1) * kPage : 0;
+    }
+    DeviceFacts f;
+    if (int st = device_facts(&f)) return st;
+
+    pdattn_cascade_plan* cp = new pdattn_cascade_plan();
+    cp->base = *base;
+    cp->d_indices = d_indices;
+    std::vector<int32_t> seqs;
+    std::vector<int> start;
+    build_cascade_nodes(h_indptr, h_indices, B, min_prefix, tree, cp->nodes, seqs, start);
+    cp->use = cp->nodes.empty() ? 0 : 1;
+    int st = PDATTN_OK;
+    if (!cp->use) {
+        if (!tree) {
+            const int P = B > 0 ? pdattn_shared_prefix_pages(h_indptr, h_indices, B) : 0;
+            if (P < 0) { delete cp; return -P; }
+            cp->Lp = P * kPage;
+        }
+        st = build_balanced_plan(h_indptr, last.data(), B, base->Hq, base->Hkv, 0, 0, false, &cp->sk);
+        cp->off_sk = 0;
+        cp->ws_bytes = cp->sk.ws_bytes;
+    } else {
+        // One prefix launch per depth (its nodes have disjoint members), sized to fill about one
+        // wave of prefix workgroups: chunk tokens ctok (a multiple of 64 in [256, 8192]) such that
+        // sum over the depth's nodes of query groups x Hkv x ceil(tokens / ctok) ~ the target.
+        // Partial columns: one range per depth, as wide as its node with the most chunks.
+        const int target = f.cus * std::max(1, f.occ_prefix[G]);
+        int depths = 0;
+        for (const CascadeNode& n : cp->nodes) depths = std::max(depths, n.depth + 1);
+        std::vector<int> depth_cols(depths, 0);
+        for (int d = 0; d < depths; ++d) {
+            double units = 0;
+            for (CascadeNode& n : cp->nodes) {
+                if (n.depth != d) continue;
+                n.qgroups = (n.ns * G + prefix_rows_per_workgroup() - 1) / prefix_rows_per_workgroup();
+                units += (double)n.qgroups * base->Hkv * (n.p1 - n.p0) * kPage;
+            }
+            int ctok = (int)(units / target);
+            ctok = std::min(std::max((ctok + 63) / 64 * 64, 256), 8192);
+            for (CascadeNode& n : cp->nodes) {
+                if (n.depth != d) continue;
+                const int Lp = (n.p1 - n.p0) * kPage;
+                n.ctok = std::min(ctok, (Lp + 63) / 64 * 64);
+                n.nchunks = (Lp + n.ctok - 1) / n.ctok;
+                depth_cols[d] = std::max(depth_cols[d], n.nchunks);
+            }
+        }
+        std::vector<int> col_of_depth(depths + 1, 0);
+        for (int d = 0; d < depths; ++d) col_of_depth[d + 1] = col_of_depth[d] + depth_cols[d];
+        for (CascadeNode& n : cp->nodes) n.col0 = col_of_depth[n.depth];
+        cp->n_extra = col_of_depth.back();
+        cp->levels = depths;
+        cp->Lp = (cp->nodes[0].p1 - cp->nodes[0].p0) * kPage;
+        // node table and per-depth item lists (items of depth 0 first)
+        std::vector<int32_t> node_tab, items;
+        for (const CascadeNode& n : cp->nodes)
+            node_tab.insert(node_tab.end(), {n.jpos, n.seq_off, n.ns, (n.p1 - n.p0) * kPage, n.ctok, n.col0, 0, 0});
+        cp->level_items.assign(depths, 0);
+        for (int d = 0; d < depths; ++d)
+            for (size_t k = 0; k < cp->nodes.size(); ++k) {
+                const CascadeNode& n = cp->nodes[k];
+                if (n.depth != d) continue;
+                for (int c = 0; c < n.nchunks; ++c)
+                    for (int qg = 0; qg < n.qgroups; ++qg) {
+                        items.insert(items.end(), {(int32_t)k, c, qg, 0});
+                        ++cp->level_items[d];
+                    }
+            }
+        cp->n_items = (int)(items.size() / 4);
+        // compacted suffix page table: pages start[b].. of every sequence
+        std::vector<int32_t> sind(B + 1, 0);
+        std::vector<int32_t> sidx;
+        for (int b = 0; b < B; ++b) {
+            for (int i = h_indptr[b] + start[b]; i < h_indptr[b + 1]; ++i) sidx.push_back(h_indices[i]);
+            sind[b + 1] = (int32_t)sidx.size();
+        }
+        st = build_balanced_plan(sind.data(), last.data(), B, base->Hq, base->Hkv, 0, 0, true, &cp->sk);
+        cp->n_suffix_idx = (int)sidx.size();
+        cp->blob = sind;
+        cp->blob.insert(cp->blob.end(), sidx.begin(), sidx.end());
+        cp->blob.insert(cp->blob.end(), seqs.begin(), seqs.end());
+        cp->n_seqs = (int)seqs.size();
+        cp->blob.insert(cp->blob.end(), node_tab.begin(), node_tab.end());
+        cp->blob.insert(cp->blob.end(), items.begin(), items.end());
+        const size_t rows = (size_t)B * base->Hq;
+        size_t off = 0;
+        cp->off_ppo = off;   off += align_up(rows * cp->n_extra * kHeadDim * sizeof(float));
+        cp->off_pplse = off; off += align_up(rows * cp->n_extra * sizeof(float));
+        cp->off_blob = off;  off += align_up(cp->blob.size() * sizeof(int32_t));
+        cp->off_sk = off;    off += cp->sk.ws_bytes;
+        cp->ws_bytes = off;
+    }
+    if (st != PDATTN_OK) {
+        pdattn_cascade_plan_destroy(cp);
+        return st;
+    }
+    *plan = cp;
     return PDATTN_OK;
 }
 
@@ -650,6 +859,11 @@ int pdattn_cascade_prefix(const pdattn_prefix_params* p, void* stream) {
     a.chunk_tokens = p->chunk_tokens;
     a.part_stride = p->part_stride;
     a.num_chunks = nchunks;
+    a.seqs = nullptr;
+    a.items = nullptr;
+    a.node_tab = nullptr;
+    a.ns = p->B;
+    a.col0 = 0;
     a.scale_log2 = p->sm_scale * 1.4426950408889634f;
     const int rows = prefix_rows_per_workgroup();
     const int qtiles = (p->B * G + rows - 1) / rows;
@@ -661,89 +875,26 @@ int pdattn_cascade_plan_create(const pdattn_decode_params* base, const int32_t* 
                                const int32_t* h_indices, const int32_t* h_lens,
                                const int32_t* d_indices, int min_prefix,
                                pdattn_cascade_plan** plan) {
-    if (!plan) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null plan output");
-    *plan = nullptr;
-    if (!base) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null base params");
-    int G = 0;
-    if (int st = check_heads(base->Hq, base->Hkv, &G)) return st;
-    const int B = base->B;
-    if (B < 0) return fail(PDATTN_ERR_INVALID_ARGUMENT, "B=%d is negative", B);
-    if (base->kv_start != 0) return fail(PDATTN_ERR_INVALID_ARGUMENT, "cascade base must have kv_start = 0");
-    if (B > 0 && (!h_indptr || !h_indices || !h_lens || !d_indices))
-        return fail(PDATTN_ERR_INVALID_ARGUMENT, "null host table / lens / device indices");
-    if (B > 0 && (!base->q || !base->k_cache || !base->v_cache || !base->kv_indptr || !base->kv_indices ||
-                  !base->kv_last_page_len))
-        return fail(PDATTN_ERR_INVALID_ARGUMENT, "null device pointer in base params");
-    if (!std::isfinite(base->sm_scale)) return fail(PDATTN_ERR_INVALID_ARGUMENT, "sm_scale is not finite");
-    // last-page lengths from the sequence lengths (ceil(L/16) pages each)
-    std::vector<int32_t> last(std::max(1, B), 0);
-    for (int b = 0; b < B; ++b) {
-        const int np = h_indptr[b + 1] - h_indptr[b];
-        if (np < 0) return fail(PDATTN_ERR_PAGE_TABLE, "indptr not monotone at %d", b);
-        if (h_lens[b] < 0 || (h_lens[b] + kPage - 1) / kPage != np)
-            return fail(PDATTN_ERR_PAGE_TABLE, "lens[%d]=%d does not match its %d pages", b, h_lens[b], np);
-        last[b] = np > 0 ? h_lens[b] - (np - 1) * kPage : 0;
-    }
-    DeviceFacts f;
-    if (int st = device_facts(&f)) return st;
+    return cascade_plan_create(base, h_indptr, h_indices, h_lens, d_indices, min_prefix, false, plan);
+}
 
-    pdattn_cascade_plan* cp = new pdattn_cascade_plan();
-    cp->base = *base;
-    const int P = B > 0 ? pdattn_shared_prefix_pages(h_indptr, h_indices, B) : 0;
-    if (P < 0) { delete cp; return -P; }
-    cp->P = P;
-    cp->Lp = P * kPage;
-    cp->use = (cp->Lp > 0 && cp->Lp >= min_prefix) ? 1 : 0;
-    int st = PDATTN_OK;
-    if (!cp->use) {
-        st = build_balanced_plan(h_indptr, last.data(), B, base->Hq, base->Hkv, 0, 0, false, &cp->sk);
-        cp->off_sk = 0;
-        cp->ws_bytes = cp->sk.ws_bytes;
-    } else {
-        // prefix chunks: about one wave of prefix workgroups, chunks of >= 256 keys, <= 8192
-        cp->qgroups = (B * G + prefix_rows_per_workgroup() - 1) / prefix_rows_per_workgroup();
-        const int target = f.cus * std::max(1, f.occ_prefix[G]);
-        int cpre = std::max(1, target / (cp->qgroups * base->Hkv));
-        cpre = std::min(cpre, std::max(1, cp->Lp / 256));
-        int ctok = ((cp->Lp + cpre - 1) / cpre + 63) / 64 * 64;
-        ctok = std::min(ctok, 8192);
-        cp->ctok = ctok;
-        cp->cpre = (cp->Lp + ctok - 1) / ctok;
-        cp->d_prefix_pages = d_indices + h_indptr[0];
-        // compacted suffix page table: pages P.. of every sequence
-        std::vector<int32_t> sind(B + 1, 0);
-        std::vector<int32_t> sidx;
-        for (int b = 0; b < B; ++b) {
-            for (int i = h_indptr[b] + P; i < h_indptr[b + 1]; ++i) sidx.push_back(h_indices[i]);
-            sind[b + 1] = (int32_t)sidx.size();
-        }
-        st = build_balanced_plan(sind.data(), last.data(), B, base->Hq, base->Hkv, 0, 0, true, &cp->sk);
-        cp->tbl = sind;
-        cp->tbl.insert(cp->tbl.end(), sidx.begin(), sidx.end());
-        const size_t rows = (size_t)B * base->Hq;
-        size_t off = 0;
-        cp->off_ppo = off;   off += align_up(rows * cp->cpre * kHeadDim * sizeof(float));
-        cp->off_pplse = off; off += align_up(rows * cp->cpre * sizeof(float));
-        cp->off_tbl = off;   off += align_up(cp->tbl.size() * sizeof(int32_t));
-        cp->off_sk = off;    off += cp->sk.ws_bytes;
-        cp->ws_bytes = off;
-    }
-    if (st != PDATTN_OK) {
-        pdattn_cascade_plan_destroy(cp);
-        return st;
-    }
-    *plan = cp;
-    return PDATTN_OK;
+int pdattn_cascade_tree_plan_create(const pdattn_decode_params* base, const int32_t* h_indptr,
+                                    const int32_t* h_indices, const int32_t* h_lens,
+                                    const int32_t* d_indices, int min_prefix,
+                                    pdattn_cascade_plan** plan) {
+    return cascade_plan_create(base, h_indptr, h_indices, h_lens, d_indices, min_prefix, true, plan);
 }
 
 int pdattn_cascade_plan_get_info(const pdattn_cascade_plan* cp, pdattn_cascade_info* info) {
     if (!cp || !info) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null pointer");
     info->use = cp->use;
     info->prefix_tokens = cp->Lp;
-    info->prefix_chunks = cp->cpre;
-    info->prefix_workgroups = cp->use ? cp->cpre * cp->qgroups * cp->base.Hkv : 0;
+    info->prefix_chunks = cp->n_extra;
+    info->prefix_workgroups = cp->n_items * cp->base.Hkv;
     info->suffix_workgroups = cp->sk.W;
     info->workspace_bytes = cp->ws_bytes;
+    info->nodes = (int)cp->nodes.size();
+    info->levels = cp->levels;
     return PDATTN_OK;
 }
 
@@ -756,42 +907,60 @@ int pdattn_cascade_decode(pdattn_cascade_plan* cp, void* out, float* lse, pdattn
     hipStream_t s = static_cast<hipStream_t>(stream);
     char* base = static_cast<char*>(ws->base);
     const pdattn_decode_params& p = cp->base;
+    float* ppo = reinterpret_cast<float*>(base + cp->off_ppo);
+    float* pplse = reinterpret_cast<float*>(base + cp->off_pplse);
     if (cp->uploaded_to != ws->base) {
         if (cp->use && !cp->pinned) {
-            hipError_t e = hipHostMalloc(&cp->pinned, cp->tbl.size() * sizeof(int32_t), hipHostMallocDefault);
+            hipError_t e = hipHostMalloc(&cp->pinned, cp->blob.size() * sizeof(int32_t), hipHostMallocDefault);
             if (e != hipSuccess) return hip_fail(e, "hipHostMalloc(cascade plan)");
-            std::memcpy(cp->pinned, cp->tbl.data(), cp->tbl.size() * sizeof(int32_t));
+            std::memcpy(cp->pinned, cp->blob.data(), cp->blob.size() * sizeof(int32_t));
         }
-        if (cp->use)
-            PD_HIP(hipMemcpyAsync(base + cp->off_tbl, cp->pinned, cp->tbl.size() * sizeof(int32_t),
+        if (cp->use) {
+            PD_HIP(hipMemcpyAsync(base + cp->off_blob, cp->pinned, cp->blob.size() * sizeof(int32_t),
                                   hipMemcpyHostToDevice, s));
+            // partial columns no node writes for a row stay empty (lse = -inf) for good
+            const size_t n_lse = (size_t)p.B * p.Hq * cp->n_extra;
+            PD_HIP(launch_fill_i32(reinterpret_cast<int32_t*>(pplse), (int32_t)0xff800000u, n_lse, s));
+        }
         if (int st = upload_plan(&cp->sk, base + cp->off_sk, cp->sk.ws_bytes, s)) return st;
         cp->uploaded_to = ws->base;
     }
     if (!cp->use)
         return run_plan(&cp->sk, p.q, p.k_cache, p.v_cache, p.kv_indptr, p.kv_indices,
-                           p.kv_last_page_len, p.sm_scale, out, lse, base + cp->off_sk, cp->sk.ws_bytes, s);
-    float* ppo = reinterpret_cast<float*>(base + cp->off_ppo);
-    float* pplse = reinterpret_cast<float*>(base + cp->off_pplse);
-    pdattn_prefix_params pp;
-    pp.q = p.q;
-    pp.k_cache = p.k_cache;
-    pp.v_cache = p.v_cache;
-    pp.prefix_pages = cp->d_prefix_pages;
-    pp.part_o = ppo;
-    pp.part_lse = pplse;
-    pp.B = p.B;
-    pp.Hq = p.Hq;
-    pp.Hkv = p.Hkv;
-    pp.prefix_len = cp->Lp;
-    pp.chunk_tokens = cp->ctok;
-    pp.part_stride = cp->cpre;
-    pp.sm_scale = p.sm_scale;
-    if (int st = pdattn_cascade_prefix(&pp, stream)) return st;
-    const int32_t* sind = reinterpret_cast<const int32_t*>(base + cp->off_tbl);
+                        p.kv_last_page_len, p.sm_scale, out, lse, base + cp->off_sk, cp->sk.ws_bytes, s);
+    const int32_t* sind = reinterpret_cast<const int32_t*>(base + cp->off_blob);
     const int32_t* sidx = sind + (p.B + 1);
+    const int32_t* dseqs = sidx + cp->n_suffix_idx;
+    const int32_t* dnodes = dseqs + cp->n_seqs;
+    const int32_t* ditems = dnodes + 8 * cp->nodes.size();
+    // one prefix launch per depth of the tree (a depth's nodes have disjoint members)
+    int item0 = 0;
+    for (int d = 0; d < cp->levels; ++d) {
+        PrefixArgs a;
+        a.q = static_cast<const _Float16*>(p.q);
+        a.k = static_cast<const uint8_t*>(p.k_cache);
+        a.v = static_cast<const uint8_t*>(p.v_cache);
+        a.prefix_pages = cp->d_indices;
+        a.seqs = dseqs;
+        a.items = ditems + 4 * (size_t)item0;
+        a.node_tab = dnodes;
+        a.part_o = ppo;
+        a.part_lse = pplse;
+        a.B = p.B;
+        a.Hq = p.Hq;
+        a.Hkv = p.Hkv;
+        a.prefix_len = 0;
+        a.chunk_tokens = 0;
+        a.part_stride = cp->n_extra;
+        a.num_chunks = cp->level_items[d];
+        a.ns = 0;
+        a.col0 = 0;
+        a.scale_log2 = p.sm_scale * 1.4426950408889634f;
+        PD_HIP(launch_cascade_prefix(a, p.Hq / p.Hkv, 1, s));
+        item0 += cp->level_items[d];
+    }
     return run_plan(&cp->sk, p.q, p.k_cache, p.v_cache, sind, sidx, p.kv_last_page_len, p.sm_scale,
-                       out, lse, base + cp->off_sk, cp->sk.ws_bytes, s, ppo, pplse, cp->cpre);
+                    out, lse, base + cp->off_sk, cp->sk.ws_bytes, s, ppo, pplse, cp->n_extra);
 }
 
 void pdattn_cascade_plan_destroy(pdattn_cascade_plan* cp) {

@@ -23,7 +23,9 @@
 // are in flight while block n is computed.
 //
 // A workgroup: 4 waves x 4 query tiles x 16 = 256 stacked query rows of one kv head, one
-// chunk of prefix keys, written as the normalized partial (o, lse) of that chunk.
+// chunk of prefix keys, written as the normalized partial (o, lse) of that chunk. The query rows
+// are those of the sequences that share the prefix (all B, or a listed subset for one node of a
+// prefix tree); chunk c of the prefix writes partial column col0 + c of each of their rows.
 #include <math.h>
 
 #include "pdattn_internal.h"
@@ -54,10 +56,13 @@ __device__ __forceinline__ f32x4 mfma16x16x32(const f16x8& a, const f16x8& b, co
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-__global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
-    __shared__ PSmem sm;
-    const int chunk = blockIdx.x, qgrp = blockIdx.y, kvh = blockIdx.z;
-    const int G = a.Hq / a.Hkv, nq = a.B * G;
+// The work of one workgroup with NT query tiles per wave. Query tile tq of a wave is tile
+// tq * PW + wave of the workgroup's rows, so a group of up to 16 * PW * NT rows occupies the first
+// NT tiles of every wave.
+template <int NT>
+__device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int chunk, int qgrp,
+                                             int kvh) {
+    const int G = a.Hq / a.Hkv, nq = a.ns * G;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int l16 = lane & 15, lg = lane >> 4;
     const int kbeg = chunk * a.chunk_tokens;
@@ -70,14 +75,14 @@ __global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
     for (int i = tid; i < npg; i += PT) sm.pg[i] = a.prefix_pages[kbeg / kPage + i];
 
     // B operands of S^T: Q[query][32 ks + 8 lg .. +7], query = l16 of tile tq
-    f16x8 qb[QT][4];
-    int qrow[QT];
+    f16x8 qb[NT][4];
+    int qrow[NT];
 #pragma unroll
-    for (int tq = 0; tq < QT; ++tq) {
-        const int qi = qgrp * QROWS + (wave * QT + tq) * 16 + l16;
+    for (int tq = 0; tq < NT; ++tq) {
+        const int qi = qgrp * QROWS + (tq * PW + wave) * 16 + l16;
         qrow[tq] = -1;
         if (qi < nq) {
-            const int b = qi / G, g = qi % G;
+            const int b = a.seqs ? a.seqs[qi / G] : qi / G, g = qi % G;
             qrow[tq] = b * a.Hq + kvh * G + g;
             const _Float16* qp = a.q + (size_t)qrow[tq] * kHeadDim + 8 * lg;
 #pragma unroll
@@ -88,10 +93,10 @@ __global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
         }
     }
 
-    f32x4 acc[QT][8];
-    float m_run[QT], l_run[QT];
+    f32x4 acc[NT][8];
+    float m_run[NT], l_run[NT];
 #pragma unroll
-    for (int tq = 0; tq < QT; ++tq) {
+    for (int tq = 0; tq < NT; ++tq) {
         m_run[tq] = -INFINITY;
         l_run[tq] = 0.f;
 #pragma unroll
@@ -155,7 +160,7 @@ __global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
         if (more) gload(kb + 1);
 
         // S^T tiles: s[tq][tk][j] = score(key 16 tk + 4 lg + j, query l16 of tile tq)
-        f32x4 s[QT][4];
+        f32x4 s[NT][4];
 #pragma unroll
         for (int tk = 0; tk < 4; ++tk) {
             f16x8 ka[4];
@@ -163,7 +168,7 @@ __global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
             for (int ks = 0; ks < 4; ++ks)
                 ka[ks] = __builtin_bit_cast(f16x8, sm.K[buf][16 * tk + l16][(4 * ks + lg) ^ l16]);
 #pragma unroll
-            for (int tq = 0; tq < QT; ++tq) {
+            for (int tq = 0; tq < NT; ++tq) {
                 f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) c = mfma16x16x32(ka[ks], qb[tq][ks], c);
@@ -173,10 +178,10 @@ __global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
 
         // online softmax (base 2) per query
         const int kbase = kbeg + kb * KB + 4 * lg;
-        float mn[QT];
+        float mn[NT];
         bool grow = false;
 #pragma unroll
-        for (int tq = 0; tq < QT; ++tq) {
+        for (int tq = 0; tq < NT; ++tq) {
             float mx = -INFINITY;
 #pragma unroll
             for (int tk = 0; tk < 4; ++tk)
@@ -194,7 +199,7 @@ __global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
         }
         if (__builtin_amdgcn_ballot_w64(grow)) {
 #pragma unroll
-            for (int tq = 0; tq < QT; ++tq) {
+            for (int tq = 0; tq < NT; ++tq) {
                 const float al = (mn[tq] > m_run[tq]) ? __builtin_amdgcn_exp2f(m_run[tq] - mn[tq]) : 1.f;
                 l_run[tq] *= al;
 #pragma unroll
@@ -202,9 +207,9 @@ __global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
                 m_run[tq] = mn[tq];
             }
         }
-        f16x8 pb[QT][2];
+        f16x8 pb[NT][2];
 #pragma unroll
-        for (int tq = 0; tq < QT; ++tq) {
+        for (int tq = 0; tq < NT; ++tq) {
             const float ms = (m_run[tq] == -INFINITY) ? 0.f : m_run[tq];
 #pragma unroll
             for (int tk = 0; tk < 4; ++tk)
@@ -230,7 +235,7 @@ __global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
                 raw[3] = sm.VT[buf][d][p0 + 9];
                 const f16x8 va = __builtin_bit_cast(f16x8, raw);
 #pragma unroll
-                for (int tq = 0; tq < QT; ++tq) acc[tq][dt] = mfma16x16x32(va, pb[tq][kb2], acc[tq][dt]);
+                for (int tq = 0; tq < NT; ++tq) acc[tq][dt] = mfma16x16x32(va, pb[tq][kb2], acc[tq][dt]);
             }
         }
 
@@ -240,12 +245,12 @@ __global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
 
     // normalized partial of this chunk
 #pragma unroll
-    for (int tq = 0; tq < QT; ++tq) {
+    for (int tq = 0; tq < NT; ++tq) {
         float L = l_run[tq];
         L += __shfl_xor(L, 16);
         L += __shfl_xor(L, 32);
         if (qrow[tq] < 0) continue;
-        const size_t slot = (size_t)qrow[tq] * a.part_stride + chunk;
+        const size_t slot = (size_t)qrow[tq] * a.part_stride + a.col0 + chunk;
         const float inv = L > 0.f ? 1.f / L : 0.f;
         float* po = a.part_o + slot * kHeadDim + 4 * lg;
 #pragma unroll
@@ -255,13 +260,48 @@ __global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
     }
 }
 
+
+__global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
+    __shared__ PSmem sm;
+    int chunk = blockIdx.x, qgrp = blockIdx.y;
+    const int kvh = blockIdx.z;
+    if (a.items) {
+        // one item of a multi-prefix launch: this workgroup's node, chunk and query group
+        const int32_t* it = a.items + 4 * (size_t)blockIdx.x;
+        const int32_t* nd = a.node_tab + 8 * (size_t)it[0];
+        chunk = it[1];
+        qgrp = it[2];
+        a.prefix_pages += nd[0];
+        a.seqs += nd[1];
+        a.ns = nd[2];
+        a.prefix_len = nd[3];
+        a.chunk_tokens = nd[4];
+        a.col0 = nd[5];
+    }
+    // query tiles per wave that hold rows of this group (the same for the whole workgroup)
+    const int rows = a.ns * (a.Hq / a.Hkv) - qgrp * QROWS;
+    if (rows > 16 * PW * 2)
+        prefix_chunk<QT>(a, sm, chunk, qgrp, kvh);
+    else if (rows > 16 * PW)
+        prefix_chunk<2>(a, sm, chunk, qgrp, kvh);
+    else
+        prefix_chunk<1>(a, sm, chunk, qgrp, kvh);
+}
+
 }  // namespace
 
 int prefix_rows_per_workgroup() { return QROWS; }
 
 hipError_t launch_cascade_prefix(const PrefixArgs& a, int G, int qtiles, hipStream_t s) {
     (void)G;
-    if (a.num_chunks <= 0 || qtiles <= 0 || a.Hkv <= 0) return hipSuccess;
+    if (a.Hkv <= 0) return hipSuccess;
+    if (a.items) {
+        // num_chunks = number of items
+        if (a.num_chunks <= 0) return hipSuccess;
+        cascade_prefix_kernel<<<dim3(a.num_chunks, 1, a.Hkv), PT, 0, s>>>(a);
+        return hipGetLastError();
+    }
+    if (a.num_chunks <= 0 || qtiles <= 0) return hipSuccess;
     dim3 grid(a.num_chunks, qtiles, a.Hkv);
     cascade_prefix_kernel<<<grid, PT, 0, s>>>(a);
     return hipGetLastError();

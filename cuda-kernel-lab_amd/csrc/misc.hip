@@ -1,4 +1,4 @@
-// misc.hip -- measurement kernels: achievable-bandwidth probe and cache flush.
+// misc.hip -- small kernels: achievable-bandwidth probe, cache flush, int32 fill.
 #include "pdattn_internal.h"
 
 namespace pdattn {
@@ -44,7 +44,19 @@ __global__ __launch_bounds__(256) void flush_kernel(u32x4* __restrict__ p, size_
     if (acc == 0x9e3779b9u) p[0].x = acc;   // keeps the loads live; never taken in practice
 }
 
+__global__ void fill_i32_kernel(int32_t* p, int32_t value, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = value;
+}
+
 }  // namespace
+
+hipError_t launch_fill_i32(int32_t* p, int32_t value, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    const size_t blocks = (n + 255) / 256;
+    fill_i32_kernel<<<(int)(blocks < 1024 ? blocks : 1024), 256, 0, s>>>(p, value, n);
+    return hipGetLastError();
+}
 
 hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, int grid, hipStream_t s) {
     stream_read_kernel<<<grid, 256, 0, s>>>(static_cast<const u32x4*>(buf), bytes / 16, sink);

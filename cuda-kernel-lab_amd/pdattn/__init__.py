@@ -40,7 +40,8 @@ EXPORTS = [
     "pdattn_plan_create", "pdattn_plan_get_info", "pdattn_plan_workspace_size",
     "pdattn_plan_get_schedule", "pdattn_plan_upload", "pdattn_plan_run", "pdattn_plan_destroy",
     "pdattn_shared_prefix_pages", "pdattn_cascade_prefix",
-    "pdattn_cascade_plan_create", "pdattn_cascade_plan_get_info", "pdattn_cascade_decode",
+    "pdattn_cascade_plan_create", "pdattn_cascade_tree_plan_create", "pdattn_cascade_plan_get_info",
+    "pdattn_cascade_decode",
     "pdattn_cascade_plan_destroy",
     "pdattn_append_kv",
     "pdattn_stream_read", "pdattn_flush_cache", "pdattn_get_device_info",
@@ -95,7 +96,8 @@ class PlanInfo(ctypes.Structure):
 class CascadeInfo(ctypes.Structure):
     _fields_ = [("use", ctypes.c_int), ("prefix_tokens", ctypes.c_int),
                 ("prefix_chunks", ctypes.c_int), ("prefix_workgroups", ctypes.c_int),
-                ("suffix_workgroups", ctypes.c_int), ("workspace_bytes", ctypes.c_size_t)]
+                ("suffix_workgroups", ctypes.c_int), ("workspace_bytes", ctypes.c_size_t),
+                ("nodes", ctypes.c_int), ("levels", ctypes.c_int)]
 
 
 class DeviceInfo(ctypes.Structure):
@@ -146,6 +148,8 @@ def lib():
         "pdattn_cascade_prefix": ([ctypes.POINTER(PrefixParams), P], I),
         "pdattn_cascade_plan_create": ([ctypes.POINTER(DecodeParams), P, P, P, P, I,
                                         ctypes.POINTER(P)], I),
+        "pdattn_cascade_tree_plan_create": ([ctypes.POINTER(DecodeParams), P, P, P, P, I,
+                                             ctypes.POINTER(P)], I),
         "pdattn_cascade_plan_get_info": ([P, ctypes.POINTER(CascadeInfo)], I),
         "pdattn_cascade_decode": ([P, P, P, ctypes.POINTER(Workspace), P], I),
         "pdattn_cascade_plan_destroy": ([P], None),
@@ -346,14 +350,17 @@ def cascade_prefix(pp: PrefixParams, stream=None):
 class CascadePlan:
     """pdattn_cascade_plan (plan_cascade, 01_decode_attention.cu:664-701)."""
 
-    def __init__(self, base: DecodeParams, indptr, indices, lens, d_indices, min_prefix: int = 256):
+    def __init__(self, base: DecodeParams, indptr, indices, lens, d_indices, min_prefix: int = 256,
+                 tree: bool = False):
+        """tree=False: the reference's single shared prefix; tree=True: a shared-prefix tree
+        (pdattn_cascade_tree_plan_create)."""
         self._h = ctypes.c_void_p()
         ip, ipp = host_i32(indptr)
         ix, ixp = host_i32(indices)
         ln, lnp = host_i32(lens)
-        _check(lib().pdattn_cascade_plan_create(ctypes.byref(base), ipp, ixp, lnp, ptr(d_indices),
-                                                min_prefix, ctypes.byref(self._h)),
-               "pdattn_cascade_plan_create")
+        fn = lib().pdattn_cascade_tree_plan_create if tree else lib().pdattn_cascade_plan_create
+        _check(fn(ctypes.byref(base), ipp, ixp, lnp, ptr(d_indices), min_prefix, ctypes.byref(self._h)),
+               "pdattn_cascade_tree_plan_create" if tree else "pdattn_cascade_plan_create")
 
     def info(self) -> CascadeInfo:
         inf = CascadeInfo()

@@ -144,6 +144,51 @@ def make_shared_prefix_batch(Lp: int, suffix, Hq: int, Hkv: int, seed: int, fill
     return bt
 
 
+def make_prefix_tree_batch(groups, suffix, Hq: int, Hkv: int, seed: int, fill: bool = True,
+                           dist: str = "normal") -> Batch:
+    """Sequences that share prefixes in a tree, with the same physical pages where shared.
+
+    groups: list of (path, tokens) for each tree node, path being the tuple of node ids from the
+    root (e.g. [((0,), 2048), ((0, 1), 4096), ((0, 2), 4096)]: node 0 shared by all, then two
+    sub-prefixes). suffix: list of (leaf path, private tokens) per sequence; a sequence's
+    context is the concatenation of the nodes on its leaf path, then its private tokens. Node
+    lengths must be whole pages; all pages are scattered randomly."""
+    node_tokens = {tuple(path): int(t) for path, t in groups}
+    if any(t % PAGE for t in node_tokens.values()):
+        raise ValueError("shared nodes must be whole pages")
+    rng = np.random.Generator(np.random.PCG64(seed))
+    node_pages = {path: t // PAGE for path, t in node_tokens.items()}
+    seqs = []
+    for leaf, priv in suffix:
+        leaf = tuple(leaf)
+        chain = [leaf[:i + 1] for i in range(len(leaf))]
+        seqs.append((chain, int(priv)))
+    lens = [sum(node_tokens[c] for c in chain) + priv for chain, priv in seqs]
+    total = sum(node_pages.values()) + sum((L + PAGE - 1) // PAGE - sum(node_pages[c] for c in chain)
+                                         for (chain, _), L in zip(seqs, lens))
+    perm = rng.permutation(total).astype(np.int32)
+    nxt = 0
+    node_ids = {}
+    for path in sorted(node_pages):
+        node_ids[path] = perm[nxt:nxt + node_pages[path]]
+        nxt += node_pages[path]
+    indptr, indices, last = [0], [], []
+    for (chain, priv), L in zip(seqs, lens):
+        np_ = (L + PAGE - 1) // PAGE
+        ids = [int(x) for c in chain for x in node_ids[c]]
+        while len(ids) < np_:
+            ids.append(int(perm[nxt]))
+            nxt += 1
+        indices += ids
+        indptr.append(indptr[-1] + np_)
+        last.append(L - (np_ - 1) * PAGE if np_ > 0 else 0)
+    bt = Batch(lens, Hq, Hkv, np.asarray(indptr, np.int32), np.asarray(indices, np.int32),
+               np.asarray(last, np.int32), total, seed)
+    if fill:
+        _fill(bt, rng, dist)
+    return bt
+
+
 def ragged_lens(B: int, lo: int, hi: int, seed: int):
     """Lengths uniform in [lo, hi] (inclusive) from a seeded PCG64 stream."""
     rng = np.random.Generator(np.random.PCG64(seed))

@@ -202,11 +202,13 @@ typedef struct pdattn_cascade_plan pdattn_cascade_plan;
 
 typedef struct pdattn_cascade_info {
     int    use;             /* 1 when a shared prefix of >= min_prefix tokens was found  */
-    int    prefix_tokens;   /* Lp                                                       */
+    int    prefix_tokens;   /* Lp (of the first node)                                   */
     int    prefix_chunks;   /* prefix partial slots per row                            */
     int    prefix_workgroups;
     int    suffix_workgroups;
     size_t workspace_bytes;
+    int    nodes;           /* shared-prefix nodes (1 for the reference's rule)        */
+    int    levels;          /* depth of the node tree                                  */
 } pdattn_cascade_info;
 
 /* Build the cascade plan (plan_cascade, 01_decode_attention.cu:664-701) from the launch block
@@ -218,6 +220,18 @@ int pdattn_cascade_plan_create(const pdattn_decode_params* base, const int32_t* 
                                const int32_t* h_indices, const int32_t* h_lens,
                                const int32_t* d_indices, int min_prefix,
                                pdattn_cascade_plan** plan);
+/* Multi-level cascade: the same decode for a batch whose sequences share prefixes in a tree (a
+ * prefix shared by all, then longer ones shared by subgroups, ...). No counterpart in the
+ * reference, which lists it as not done (README.md:73). The planner walks the host page table:
+ * a group of sequences that hold the same page at some position extends a node while every
+ * member holds the same page and keeps a page of its own after it; a node of at least
+ * min_prefix tokens is decoded once for all its members on fp16 MFMA, and the group splits by
+ * the page that follows. Each sequence's remaining pages go through the balanced decode, and
+ * every row merges its suffix partial with the partials of all its nodes, in a fixed order. */
+int pdattn_cascade_tree_plan_create(const pdattn_decode_params* base, const int32_t* h_indptr,
+                                    const int32_t* h_indices, const int32_t* h_lens,
+                                    const int32_t* d_indices, int min_prefix,
+                                    pdattn_cascade_plan** plan);
 int pdattn_cascade_plan_get_info(const pdattn_cascade_plan* plan, pdattn_cascade_info* info);
 /* Prefix kernel, suffix decode and merge on `stream` (cascade_decode, 01_decode_attention.cu:703-712).
  * The first call with a given workspace uploads the plan's schedule into it (stream-ordered). */

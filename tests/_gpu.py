@@ -85,10 +85,10 @@ def run_partials(db: DeviceBatch, num_chunks: int, chunk_tokens: int, kv_start: 
     return po.cpu().numpy().astype(np.float64), pl.cpu().numpy().astype(np.float64)
 
 
-def run_cascade(db: DeviceBatch, min_prefix: int = 256):
+def run_cascade(db: DeviceBatch, min_prefix: int = 256, tree: bool = False):
     bt = db.bt
     base = db.params()
-    cp = pdattn.CascadePlan(base, bt.indptr, bt.indices, bt.lens, db.indices, min_prefix)
+    cp = pdattn.CascadePlan(base, bt.indptr, bt.indices, bt.lens, db.indices, min_prefix, tree)
     ws = pdattn.Workspace()
     try:
         cp.decode(db.out, db.lse, ws)

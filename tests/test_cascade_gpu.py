@@ -114,3 +114,41 @@ def test_short_prefix_below_min_prefix_falls_back():
     assert info.use == 0
     check_out(o, ro)
     check_lse(l, rl)
+
+
+# ---- multi-level cascade (shared-prefix tree) ----------------------------------------------------
+# (label, nodes [(path, tokens)], sequences [(leaf path, private tokens)], Hq, Hkv, nodes, levels)
+TREE_CASES = [
+    ("two levels, two groups", [((0,), 64), ((0, 1), 128), ((0, 2), 32)],
+     [((0, 1), 5), ((0, 1), 40), ((0, 2), 1), ((0,), 17), ((0, 2), 16)], 8, 2, 3, 2),
+    ("three levels, G=4", [((0,), 256), ((0, 1), 512), ((0, 1, 2), 256), ((0, 3), 64)],
+     [((0, 1, 2), 100), ((0, 1, 2), 3), ((0, 1), 50), ((0, 3), 7), ((0, 3), 300), ((0,), 1)],
+     32, 8, 4, 3),
+    ("forest of two roots", [((0,), 256), ((1,), 512)],
+     [((0,), 10), ((0,), 20), ((1,), 5), ((1,), 300), ((), 77)], 32, 8, 2, 1),
+    ("system prompt + 4 documents", [((0,), 1024)] + [((0, g), 512) for g in range(1, 5)],
+     [((0, g), 64 + 17 * i) for g in range(1, 5) for i in range(4)], 32, 8, 5, 2),
+]
+
+
+@pytest.mark.parametrize("case", TREE_CASES, ids=[c[0] for c in TREE_CASES])
+def test_tree_cascade_matches_oracle(case):
+    import _gpu
+    label, nodes, seqs, Hq, Hkv, n_nodes, levels = case
+    bt = inputs.make_prefix_tree_batch(nodes, seqs, Hq, Hkv, seed=51)
+    print(f"tree cascade: {label}", flush=True)
+    o, l, info = _gpu.run_cascade(_gpu.DeviceBatch(bt), min_prefix=16, tree=True)
+    assert info.use == 1 and info.nodes == n_nodes and info.levels == levels
+    ro, rl = _ref(bt)
+    check_out(o, ro, tag=label)
+    check_lse(l, rl, tag=label)
+
+
+def test_tree_cascade_without_sharing_falls_back():
+    import _gpu
+    bt = inputs.make_batch([100, 37, 300], 32, 8, seed=52)
+    o, l, info = _gpu.run_cascade(_gpu.DeviceBatch(bt), min_prefix=16, tree=True)
+    assert info.use == 0 and info.nodes == 0
+    ro, rl = _ref(bt)
+    check_out(o, ro)
+    check_lse(l, rl)

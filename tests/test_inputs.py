@@ -38,3 +38,20 @@ def test_ragged_lengths_are_seeded():
     a = inputs.ragged_lens(64, 256, 4096, 11)
     assert a == inputs.ragged_lens(64, 256, 4096, 11)
     assert min(a) >= 256 and max(a) <= 4096
+
+
+def test_prefix_tree_batch():
+    """Node pages are shared exactly along each sequence's path; private pages are its own."""
+    groups = [((0,), 32), ((0, 1), 48), ((0, 2), 16)]
+    seqs = [((0, 1), 5), ((0, 1), 16), ((0, 2), 1), ((0,), 20)]
+    bt = inputs.make_prefix_tree_batch(groups, seqs, 8, 2, seed=7, fill=False)
+    assert bt.lens == [85, 96, 49, 52]
+    rows = [bt.indices[bt.indptr[b]:bt.indptr[b + 1]].tolist() for b in range(bt.B)]
+    root = rows[0][:2]
+    assert all(r[:2] == root for r in rows)
+    assert rows[0][2:5] == rows[1][2:5]                     # node (0, 1)
+    assert rows[2][2] not in rows[0] and rows[3][2] not in rows[0] + rows[2]
+    flat = sorted(bt.indices.tolist())
+    assert sorted(set(flat)) == list(range(bt.num_pages))   # every page used, ids in range
+    # each page is used by one sequence, or by the members of the one node that owns it
+    assert bt.num_pages == 2 + 3 + 1 + (1 + 1 + 1 + 2)
