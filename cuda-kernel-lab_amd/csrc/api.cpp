@@ -575,10 +575,8 @@ int cascade_plan_create(const pdattn_decode_params* base, const int32_t* h_indpt
         cp->n_extra = col_of_depth.back();
         cp->levels = depths;
         cp->Lp = (cp->nodes[0].p1 - cp->nodes[0].p0) * kPage;
-        // node table and per-depth item lists (items of depth 0 first)
-        std::vector<int32_t> node_tab, items;
-        for (const CascadeNode& n : cp->nodes)
-            node_tab.insert(node_tab.end(), {n.jpos, n.seq_off, n.ns, (n.p1 - n.p0) * kPage, n.ctok, n.col0, 0, 0});
+        // per-depth item lists (items of depth 0 first), each item carrying its node's fields
+        std::vector<int32_t> items;
         cp->level_items.assign(depths, 0);
         for (int d = 0; d < depths; ++d)
             for (size_t k = 0; k < cp->nodes.size(); ++k) {
@@ -586,11 +584,12 @@ int cascade_plan_create(const pdattn_decode_params* base, const int32_t* h_indpt
                 if (n.depth != d) continue;
                 for (int c = 0; c < n.nchunks; ++c)
                     for (int qg = 0; qg < n.qgroups; ++qg) {
-                        items.insert(items.end(), {(int32_t)k, c, qg, 0});
+                        items.insert(items.end(), {n.jpos, n.seq_off, n.ns, (n.p1 - n.p0) * kPage,
+                                                   n.ctok, n.col0, c, qg});
                         ++cp->level_items[d];
                     }
             }
-        cp->n_items = (int)(items.size() / 4);
+        cp->n_items = (int)(items.size() / 8);
         // compacted suffix page table: pages start[b].. of every sequence
         std::vector<int32_t> sind(B + 1, 0);
         std::vector<int32_t> sidx;
@@ -604,7 +603,6 @@ int cascade_plan_create(const pdattn_decode_params* base, const int32_t* h_indpt
         cp->blob.insert(cp->blob.end(), sidx.begin(), sidx.end());
         cp->blob.insert(cp->blob.end(), seqs.begin(), seqs.end());
         cp->n_seqs = (int)seqs.size();
-        cp->blob.insert(cp->blob.end(), node_tab.begin(), node_tab.end());
         cp->blob.insert(cp->blob.end(), items.begin(), items.end());
         const size_t rows = (size_t)B * base->Hq;
         size_t off = 0;
@@ -861,7 +859,6 @@ int pdattn_cascade_prefix(const pdattn_prefix_params* p, void* stream) {
     a.num_chunks = nchunks;
     a.seqs = nullptr;
     a.items = nullptr;
-    a.node_tab = nullptr;
     a.ns = p->B;
     a.col0 = 0;
     a.scale_log2 = p->sm_scale * 1.4426950408889634f;
@@ -931,8 +928,7 @@ int pdattn_cascade_decode(pdattn_cascade_plan* cp, void* out, float* lse, pdattn
     const int32_t* sind = reinterpret_cast<const int32_t*>(base + cp->off_blob);
     const int32_t* sidx = sind + (p.B + 1);
     const int32_t* dseqs = sidx + cp->n_suffix_idx;
-    const int32_t* dnodes = dseqs + cp->n_seqs;
-    const int32_t* ditems = dnodes + 8 * cp->nodes.size();
+    const int32_t* ditems = dseqs + cp->n_seqs;
     // one prefix launch per depth of the tree (a depth's nodes have disjoint members)
     int item0 = 0;
     for (int d = 0; d < cp->levels; ++d) {
@@ -942,8 +938,7 @@ int pdattn_cascade_decode(pdattn_cascade_plan* cp, void* out, float* lse, pdattn
         a.v = static_cast<const uint8_t*>(p.v_cache);
         a.prefix_pages = cp->d_indices;
         a.seqs = dseqs;
-        a.items = ditems + 4 * (size_t)item0;
-        a.node_tab = dnodes;
+        a.items = ditems + 8 * (size_t)item0;
         a.part_o = ppo;
         a.part_lse = pplse;
         a.B = p.B;

@@ -22,10 +22,13 @@
 // PV product is two conflict-free 8-byte reads. Two LDS buffers: the global loads of block n+1
 // are in flight while block n is computed.
 //
-// A workgroup: 4 waves x 4 query tiles x 16 = 256 stacked query rows of one kv head, one
-// chunk of prefix keys, written as the normalized partial (o, lse) of that chunk. The query rows
-// are those of the sequences that share the prefix (all B, or a listed subset for one node of a
-// prefix tree); chunk c of the prefix writes partial column col0 + c of each of their rows.
+// A workgroup: 8 waves x 2 query tiles x 16 = 256 stacked query rows of one kv head, one chunk
+// of prefix keys, written as the normalized partial (o, lse) of that chunk. The query rows are
+// those of the sequences that share the prefix (all B, or a listed subset for one node of a
+// prefix tree); chunk c of the prefix writes partial column col0 + c of each of their rows. Two
+// waves per SIMD: one wave's softmax (VALU) runs while the other's products occupy the matrix
+// core, and the per-wave register budget (~200) keeps the accumulators out of AGPRs, so the
+// softmax rescale touches them in place.
 #include <math.h>
 
 #include "pdattn_internal.h"
@@ -38,9 +41,9 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLn2 = 0.69314718055994531f;
-constexpr int PW = 4;               // waves per workgroup
+constexpr int PW = 8;               // waves per workgroup
 constexpr int PT = PW * 64;         // threads per workgroup
-constexpr int QT = 4;               // 16-query tiles per wave
+constexpr int QT = 2;               // 16-query tiles per wave
 constexpr int QROWS = PW * QT * 16; // stacked query rows per workgroup
 constexpr int KB = 64;              // keys per LDS block
 constexpr int VTS = 33;             // V^T row stride in dwords (32 key pairs + 1 pad)
@@ -50,6 +53,7 @@ struct PSmem {
     u32x4 K[2][KB][16];              // [key][chunk ^ (key & 15)], 16 bytes = 8 dims per chunk
     uint32_t VT[2][kHeadDim][VTS];   // [dim][key pair]: low half key 2p, high half key 2p+1
     int pg[MAXPG];                   // physical pages of this chunk
+    int sq[QROWS];                   // sequences of this group's query rows (one per G rows)
 };
 
 __device__ __forceinline__ f32x4 mfma16x16x32(const f16x8& a, const f16x8& b, const f32x4& c) {
@@ -63,7 +67,7 @@ template <int NT>
 __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int chunk, int qgrp,
                                              int kvh) {
     const int G = a.Hq / a.Hkv, nq = a.ns * G;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int l16 = lane & 15, lg = lane >> 4;
     const int kbeg = chunk * a.chunk_tokens;
     const int kend = min(a.prefix_len, kbeg + a.chunk_tokens);
@@ -71,27 +75,73 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
     const int npg = (nkeys + kPage - 1) / kPage;
     const int nblk = (nkeys + KB - 1) / KB;
     const size_t page_bytes = (size_t)kPage * a.Hkv * 256;
+    const int s0 = qgrp * (QROWS / G);                 // first member of this query group
+    const int nsq = min(QROWS / G, a.ns - s0);
 
+    // page ids and member ids in one round trip
     for (int i = tid; i < npg; i += PT) sm.pg[i] = a.prefix_pages[kbeg / kPage + i];
+    for (int j = tid; j < nsq; j += PT) sm.sq[j] = a.seqs ? a.seqs[s0 + j] : s0 + j;
 
-    // B operands of S^T: Q[query][32 ks + 8 lg .. +7], query = l16 of tile tq
+    // Staging: thread t moves 16-byte chunk sc = t & 15 of K rows sr and sr + 32 and of the V key
+    // pair (2 sr, 2 sr + 1), sr = t >> 4. Keys past the chunk read the last valid key instead (a
+    // real, finite row): their scores are masked to -inf below, so their weights are exactly 0.
+    const int sc = tid & 15, sr = tid >> 4;
+    u32x4 kst[2], vst[2];
+    auto gload = [&](int kb) {
+        const int key0 = kbeg + kb * KB;
+        int key[4] = {key0 + sr, key0 + sr + 32, key0 + 2 * sr, key0 + 2 * sr + 1};
+        uint32_t pid[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            key[i] = min(key[i], kend - 1);
+            pid[i] = (uint32_t)sm.pg[(key[i] - kbeg) >> 4];
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            kst[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+                a.k + pid[i] * page_bytes + (size_t)(((key[i] & 15) * a.Hkv + kvh) * 256 + sc * 16)));
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            vst[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+                a.v + pid[2 + i] * page_bytes + (size_t)(((key[2 + i] & 15) * a.Hkv + kvh) * 256 + sc * 16)));
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int n = sr + 32 * i;
+            sm.K[buf][n][sc ^ (n & 15)] = kst[i];
+        }
+        const u32x4 lo = vst[0], hi = vst[1];   // keys 2 sr and 2 sr + 1, dims 8 sc .. +7
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            sm.VT[buf][8 * sc + 2 * e][sr] = __builtin_amdgcn_perm(hi[e], lo[e], 0x05040100u);
+            sm.VT[buf][8 * sc + 2 * e + 1][sr] = __builtin_amdgcn_perm(hi[e], lo[e], 0x07060302u);
+        }
+    };
+
+    __syncthreads();   // page ids, member ids
+    if (nblk > 0) gload(0);
+
+    // B operands of S^T: Q[query][32 ks + 8 lg .. +7], query = l16 of tile tq; loaded behind the
+    // first block (rows past the group read its last row and are zeroed)
     f16x8 qb[NT][4];
     int qrow[NT];
 #pragma unroll
     for (int tq = 0; tq < NT; ++tq) {
-        const int qi = qgrp * QROWS + (tq * PW + wave) * 16 + l16;
-        qrow[tq] = -1;
-        if (qi < nq) {
-            const int b = a.seqs ? a.seqs[qi / G] : qi / G, g = qi % G;
-            qrow[tq] = b * a.Hq + kvh * G + g;
-            const _Float16* qp = a.q + (size_t)qrow[tq] * kHeadDim + 8 * lg;
+        const int r = (tq * PW + wave) * 16 + l16;    // row within the group
+        const bool ok = qgrp * QROWS + r < nq;
+        const int rr = ok ? r : nsq * G - 1;
+        const int b = sm.sq[rr / G], g = rr % G;
+        const _Float16* qp = a.q + ((size_t)b * a.Hq + kvh * G + g) * kHeadDim + 8 * lg;
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks) qb[tq][ks] = *reinterpret_cast<const f16x8*>(qp + 32 * ks);
-        } else {
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) qb[tq][ks] = f16x8{};
-        }
+        for (int ks = 0; ks < 4; ++ks) qb[tq][ks] = *reinterpret_cast<const f16x8*>(qp + 32 * ks);
+        qrow[tq] = ok ? b * a.Hq + kvh * G + g : -1;
     }
+#pragma unroll
+    for (int tq = 0; tq < NT; ++tq)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+            if (qrow[tq] < 0) qb[tq][ks] = f16x8{};
 
     f32x4 acc[NT][8];
     float m_run[NT], l_run[NT];
@@ -103,55 +153,7 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
         for (int dt = 0; dt < 8; ++dt) acc[tq][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    // staging: K rows tid/16 + 16 i, chunk tid%16; V rows 2 kp (+1) + 32 s, kp = tid/16
-    const int sc = tid & 15, sr = tid >> 4;
-    u32x4 kst[4], vst[4];
-    auto gload = [&](int kb) {
-        const int key0 = kbeg + kb * KB;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int key = key0 + sr + 16 * i;
-            kst[i] = u32x4{0u, 0u, 0u, 0u};
-            if (key < kend) {
-                const size_t pid = (uint32_t)sm.pg[(key - kbeg) >> 4];
-                kst[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-                    a.k + pid * page_bytes + (size_t)(((key & 15) * a.Hkv + kvh) * 256 + sc * 16)));
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int key = key0 + 2 * sr + (i & 1) + 32 * (i >> 1);
-            vst[i] = u32x4{0u, 0u, 0u, 0u};
-            if (key < kend) {
-                const size_t pid = (uint32_t)sm.pg[(key - kbeg) >> 4];
-                vst[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-                    a.v + pid * page_bytes + (size_t)(((key & 15) * a.Hkv + kvh) * 256 + sc * 16)));
-            }
-        }
-    };
-    auto lstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int n = sr + 16 * i;
-            sm.K[buf][n][sc ^ (n & 15)] = kst[i];
-        }
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const u32x4 lo = vst[2 * s], hi = vst[2 * s + 1];  // keys 2p and 2p+1, dims 8 sc .. +7
-            const int p = sr + 16 * s;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                sm.VT[buf][8 * sc + 2 * e][p] = __builtin_amdgcn_perm(hi[e], lo[e], 0x05040100u);
-                sm.VT[buf][8 * sc + 2 * e + 1][p] = __builtin_amdgcn_perm(hi[e], lo[e], 0x07060302u);
-            }
-        }
-    };
-
-    __syncthreads();  // page ids
-    if (nblk > 0) {
-        gload(0);
-        lstore(0);
-    }
+    if (nblk > 0) lstore(0);
     __syncthreads();
 
     for (int kb = 0; kb < nblk; ++kb) {
@@ -260,30 +262,28 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
     }
 }
 
-
 __global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
     __shared__ PSmem sm;
     int chunk = blockIdx.x, qgrp = blockIdx.y;
     const int kvh = blockIdx.z;
     if (a.items) {
-        // one item of a multi-prefix launch: this workgroup's node, chunk and query group
-        const int32_t* it = a.items + 4 * (size_t)blockIdx.x;
-        const int32_t* nd = a.node_tab + 8 * (size_t)it[0];
-        chunk = it[1];
-        qgrp = it[2];
-        a.prefix_pages += nd[0];
-        a.seqs += nd[1];
-        a.ns = nd[2];
-        a.prefix_len = nd[3];
-        a.chunk_tokens = nd[4];
-        a.col0 = nd[5];
+        // one item of a multi-prefix launch: {page-table position of the node's first page,
+        // offset of its members in seqs, members, tokens, chunk tokens, first partial column,
+        // chunk, query group}
+        const int32_t* it = a.items + 8 * (size_t)blockIdx.x;
+        a.prefix_pages += it[0];
+        a.seqs += it[1];
+        a.ns = it[2];
+        a.prefix_len = it[3];
+        a.chunk_tokens = it[4];
+        a.col0 = it[5];
+        chunk = it[6];
+        qgrp = it[7];
     }
     // query tiles per wave that hold rows of this group (the same for the whole workgroup)
     const int rows = a.ns * (a.Hq / a.Hkv) - qgrp * QROWS;
-    if (rows > 16 * PW * 2)
+    if (rows > 16 * PW)
         prefix_chunk<QT>(a, sm, chunk, qgrp, kvh);
-    else if (rows > 16 * PW)
-        prefix_chunk<2>(a, sm, chunk, qgrp, kvh);
     else
         prefix_chunk<1>(a, sm, chunk, qgrp, kvh);
 }

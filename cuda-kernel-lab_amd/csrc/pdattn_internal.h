@@ -90,11 +90,10 @@ struct PrefixArgs {
     const int32_t*  prefix_pages;
     const int32_t*  seqs;         // the ns sequences sharing the prefix (null: 0 .. ns-1)
     // Several prefixes in one launch (the nodes of one depth of a prefix tree): workgroup x
-    // takes item items[x] = {node, chunk, query group, 0} of node node_tab[node] = {page-table
-    // position of its first page, offset of its members in seqs, members, tokens, chunk tokens,
-    // first partial column, 0, 0}; prefix_pages is then the whole page table. Null: one prefix.
+    // takes item items[8 x ..] = {page-table position of its node's first page, offset of the
+    // node's members in seqs, members, tokens, chunk tokens, first partial column, chunk, query
+    // group}; prefix_pages is then the whole page table. Null: one prefix.
     const int32_t*  items;
-    const int32_t*  node_tab;
     float*          part_o;       // rows b*Hq + h, slot row*part_stride + col0 + chunk
     float*          part_lse;
     int B, Hq, Hkv, prefix_len, chunk_tokens, part_stride, num_chunks;
