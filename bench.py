@@ -273,12 +273,21 @@ def cascade_workload(timer, args):
     cp = pdattn.CascadePlan(base, bt3.indptr, bt3.indices, bt3.lens, t3["indices"])
     cws = pdattn.Workspace()
     cp.decode(t3["out"], t3["lse"], cws, s)  # uploads the schedule
-    f3c = lambda: cp.decode(t3["out"], t3["lse"], cws, s)  # noqa: E731
-    w3n, w3c = timer.run([f3n, f3c], args.steps, args.warmup, rounds=3)
-    mn, mc = statistics.median(w3n), statistics.median(w3c)
+
+    def f3c():
+        cp.set_overlap(False)    # every launch on the caller's stream (the default)
+        cp.decode(t3["out"], t3["lse"], cws, s)
+
+    def f3o():
+        cp.set_overlap(True)     # prefix launches forked onto the plan's second stream
+        cp.decode(t3["out"], t3["lse"], cws, s)
+    w3n, w3c, w3o = timer.run([f3n, f3c, f3o], args.steps, args.warmup, rounds=3)
+    mn, mc, mo = statistics.median(w3n), statistics.median(w3c), statistics.median(w3o)
+    cp.set_overlap(False)
     ci = cp.info()
     out = {"non_shared_us": round(mn * 1e3, 2), "cascade_us": round(mc * 1e3, 2),
-           "speedup": round(mn / mc, 2), "prefix_chunks": ci.prefix_chunks,
+           "speedup": round(mn / mc, 2), "cascade_two_streams_us": round(mo * 1e3, 2),
+           "prefix_chunks": ci.prefix_chunks,
            "prefix_workgroups": ci.prefix_workgroups, "suffix_workgroups": ci.suffix_workgroups}
     cp.close()
     pdattn.workspace_release(cws)

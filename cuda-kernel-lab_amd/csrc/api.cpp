@@ -204,6 +204,11 @@ struct pdattn_cascade_plan {
     void* pinned = nullptr;
     size_t off_ppo = 0, off_pplse = 0, off_blob = 0, off_sk = 0, ws_bytes = 0;
     const void* uploaded_to = nullptr;
+    // prefix launches on a second stream, concurrent with the suffix decode (created on first
+    // use); off by default: on MI355X the fork / join events cost more than the overlap recovers
+    int overlap = 0;
+    hipStream_t aux = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
 };
 
 namespace {
@@ -375,11 +380,13 @@ int upload_plan(pdattn_plan* pl, void* ws, size_t bytes, hipStream_t s) {
     return PDATTN_OK;
 }
 
-// Balanced decode launch, then (when the plan lists any) the merge launch.
+// Balanced decode launch, then (when the plan lists any) the merge launch. With `join`, the
+// stream waits for that event between the two (the extra partials come from another stream).
 int run_plan(const pdattn_plan* pl, const void* q, const void* k, const void* v,
              const int32_t* indptr, const int32_t* indices, const int32_t* last, float sm_scale,
              void* out, float* lse, void* ws, size_t bytes, hipStream_t s,
-             const float* extra_o = nullptr, const float* extra_lse = nullptr, int n_extra = 0) {
+             const float* extra_o = nullptr, const float* extra_lse = nullptr, int n_extra = 0,
+             hipEvent_t join = nullptr) {
     if (ws != pl->uploaded_to)
         return fail(PDATTN_ERR_NOT_READY, "plan was not uploaded into this workspace");
     if (bytes < pl->ws_bytes)
@@ -411,6 +418,7 @@ int run_plan(const pdattn_plan* pl, const void* q, const void* k, const void* v,
         a.scale_log2 = sm_scale * 1.4426950408889634f;
         PD_HIP(launch_decode_balanced(a, pl->G, s));
     }
+    if (join) PD_HIP(hipStreamWaitEvent(s, join, 0));
     if (pl->n_entries) {
         MergeArgs m;
         m.list = reinterpret_cast<const int32_t*>(base + pl->off_list);
@@ -929,7 +937,20 @@ int pdattn_cascade_decode(pdattn_cascade_plan* cp, void* out, float* lse, pdattn
     const int32_t* sidx = sind + (p.B + 1);
     const int32_t* dseqs = sidx + cp->n_suffix_idx;
     const int32_t* ditems = dseqs + cp->n_seqs;
-    // one prefix launch per depth of the tree (a depth's nodes have disjoint members)
+    // One prefix launch per depth of the tree (a depth's nodes have disjoint members). With overlap
+    // the prefix launches run on the plan's second stream while the suffix decode runs on `s`;
+    // `s` waits for them before the merge, so the step stays one fork / join (graph-capturable).
+    hipStream_t ps = s;
+    if (cp->overlap) {
+        if (!cp->aux) {
+            PD_HIP(hipStreamCreateWithFlags(&cp->aux, hipStreamNonBlocking));
+            PD_HIP(hipEventCreateWithFlags(&cp->ev_fork, hipEventDisableTiming));
+            PD_HIP(hipEventCreateWithFlags(&cp->ev_join, hipEventDisableTiming));
+        }
+        PD_HIP(hipEventRecord(cp->ev_fork, s));
+        PD_HIP(hipStreamWaitEvent(cp->aux, cp->ev_fork, 0));
+        ps = cp->aux;
+    }
     int item0 = 0;
     for (int d = 0; d < cp->levels; ++d) {
         PrefixArgs a;
@@ -951,15 +972,27 @@ int pdattn_cascade_decode(pdattn_cascade_plan* cp, void* out, float* lse, pdattn
         a.ns = 0;
         a.col0 = 0;
         a.scale_log2 = p.sm_scale * 1.4426950408889634f;
-        PD_HIP(launch_cascade_prefix(a, p.Hq / p.Hkv, 1, s));
+        PD_HIP(launch_cascade_prefix(a, p.Hq / p.Hkv, 1, ps));
         item0 += cp->level_items[d];
     }
+    if (cp->overlap) PD_HIP(hipEventRecord(cp->ev_join, ps));
     return run_plan(&cp->sk, p.q, p.k_cache, p.v_cache, sind, sidx, p.kv_last_page_len, p.sm_scale,
-                    out, lse, base + cp->off_sk, cp->sk.ws_bytes, s, ppo, pplse, cp->n_extra);
+                    out, lse, base + cp->off_sk, cp->sk.ws_bytes, s, ppo, pplse, cp->n_extra,
+                    cp->overlap ? cp->ev_join : nullptr);
+}
+
+int pdattn_cascade_set_overlap(pdattn_cascade_plan* cp, int enable) {
+    if (!cp) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null plan");
+    cp->overlap = enable ? 1 : 0;
+    return PDATTN_OK;
 }
 
 void pdattn_cascade_plan_destroy(pdattn_cascade_plan* cp) {
     if (!cp) return;
+    if (cp->aux) (void)hipStreamSynchronize(cp->aux);
+    if (cp->ev_fork) (void)hipEventDestroy(cp->ev_fork);
+    if (cp->ev_join) (void)hipEventDestroy(cp->ev_join);
+    if (cp->aux) (void)hipStreamDestroy(cp->aux);
     free_plan_storage(&cp->sk);
     if (cp->pinned) (void)hipHostFree(cp->pinned);
     delete cp;

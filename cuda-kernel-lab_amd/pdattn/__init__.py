@@ -41,7 +41,7 @@ EXPORTS = [
     "pdattn_plan_get_schedule", "pdattn_plan_upload", "pdattn_plan_run", "pdattn_plan_destroy",
     "pdattn_shared_prefix_pages", "pdattn_cascade_prefix",
     "pdattn_cascade_plan_create", "pdattn_cascade_tree_plan_create", "pdattn_cascade_plan_get_info",
-    "pdattn_cascade_decode",
+    "pdattn_cascade_decode", "pdattn_cascade_set_overlap",
     "pdattn_cascade_plan_destroy",
     "pdattn_append_kv",
     "pdattn_stream_read", "pdattn_flush_cache", "pdattn_get_device_info",
@@ -152,6 +152,7 @@ def lib():
                                              ctypes.POINTER(P)], I),
         "pdattn_cascade_plan_get_info": ([P, ctypes.POINTER(CascadeInfo)], I),
         "pdattn_cascade_decode": ([P, P, P, ctypes.POINTER(Workspace), P], I),
+        "pdattn_cascade_set_overlap": ([P, I], I),
         "pdattn_cascade_plan_destroy": ([P], None),
         "pdattn_append_kv": ([P, P, P, P, P, P, P, P, I, I, I, P, P], I),
         "pdattn_stream_read": ([P, S, P, P], I),
@@ -370,6 +371,11 @@ class CascadePlan:
     def decode(self, out, lse, ws: Workspace, stream=None):
         _check(lib().pdattn_cascade_decode(self._h, ptr(out), ptr(lse), ctypes.byref(ws), stream_ptr(stream)),
                "pdattn_cascade_decode")
+
+    def set_overlap(self, enable: bool):
+        """Prefix launches on the plan's second stream, concurrent with the suffix decode (the
+        default), or every launch on the caller's stream (pdattn_cascade_set_overlap)."""
+        _check(lib().pdattn_cascade_set_overlap(self._h, int(bool(enable))), "pdattn_cascade_set_overlap")
 
     def close(self):
         if self._h:

@@ -237,6 +237,15 @@ int pdattn_cascade_plan_get_info(const pdattn_cascade_plan* plan, pdattn_cascade
  * The first call with a given workspace uploads the plan's schedule into it (stream-ordered). */
 int pdattn_cascade_decode(pdattn_cascade_plan* plan, void* out, float* lse, pdattn_workspace* ws,
                           void* stream);
+/* Prefix/suffix overlap (off by default). With enable = 1, pdattn_cascade_decode forks the prefix
+ * launches onto a second stream owned by the plan (created on first use, default priority) and
+ * joins it back into `stream` before the merge, so the prefix MFMA pass and the suffix decode can
+ * run concurrently; the step stays graph-capturable. The results are bitwise the same either way.
+ * The reference lists this as not done (README.md:73). On MI355X the cross-queue fork and join
+ * each add several microseconds and the two kernels cannot share a CU (registers), so the single
+ * stream is faster at the benchmark's shapes; the option is for callers whose prefix pass is long
+ * enough to hide them. */
+int pdattn_cascade_set_overlap(pdattn_cascade_plan* plan, int enable);
 void pdattn_cascade_plan_destroy(pdattn_cascade_plan* plan);
 
 /* ---- paged KV append ---------------------------------------------------------------------- */

@@ -152,3 +152,45 @@ def test_tree_cascade_without_sharing_falls_back():
     ro, rl = _ref(bt)
     check_out(o, ro)
     check_lse(l, rl)
+
+
+@pytest.mark.parametrize("tree", [False, True], ids=["single-level", "tree"])
+def test_overlap_on_and_off_bitwise_equal(tree):
+    """Prefix launches forked onto the plan's second stream or on the caller's stream (the
+    default): the same kernels, so the same bits; both against the oracle."""
+    import torch
+
+    import _gpu
+    import pdattn
+    if tree:
+        nodes = [((0,), 256), ((0, 1), 512), ((0, 2), 128)]
+        seqs = [((0, 1), 40), ((0, 1), 3), ((0, 2), 100), ((0, 2), 16), ((0,), 77)]
+        bt = inputs.make_prefix_tree_batch(nodes, seqs, 32, 8, seed=61)
+    else:
+        bt = inputs.make_shared_prefix_batch(1024, [1] * 70, 32, 8, seed=62)
+    db = _gpu.DeviceBatch(bt)
+    print(f"cascade overlap on/off: tree={tree}", flush=True)
+    cp = pdattn.CascadePlan(db.params(), bt.indptr, bt.indices, bt.lens, db.indices, 16, tree)
+    ws = pdattn.Workspace()
+    got = []
+    try:
+        assert cp.info().use == 1
+        s = torch.cuda.current_stream()
+        for enable in (True, False, True):
+            cp.set_overlap(enable)
+            db.out.fill_(float("nan"))
+            db.lse.fill_(float("nan"))
+            cp.decode(db.out, db.lse, ws, s)
+            torch.cuda.synchronize()
+            got.append((db.out.clone(), db.lse.clone()))
+    finally:
+        cp.close()
+        pdattn.workspace_release(ws)
+    for o, l in got[1:]:
+        assert torch.equal(o.view(torch.int16), got[0][0].view(torch.int16))
+        assert torch.equal(l.view(torch.int32), got[0][1].view(torch.int32))
+    o = got[0][0].float().cpu().numpy().astype(np.float64)
+    l = got[0][1].cpu().numpy().astype(np.float64)
+    ro, rl = _ref(bt)
+    check_out(o, ro)
+    check_lse(l, rl)

@@ -80,6 +80,29 @@ def test_cascade_graph():
     pdattn.workspace_release(ws)
 
 
+def test_cascade_two_streams_graph():
+    """The cascade with its prefix launches forked onto the plan's second stream: the fork / join
+    events are captured into the graph along with the launches."""
+    bt = inputs.make_shared_prefix_batch(512, [40, 1, 300, 17, 64], 32, 8, seed=36)
+    db = DeviceBatch(bt)
+    print("graph: cascade, two streams", flush=True)
+    cp = pdattn.CascadePlan(db.params(), bt.indptr, bt.indices, bt.lens, db.indices, 256)
+    assert cp.info().use == 1
+    cp.set_overlap(True)
+    ws = pdattn.Workspace()
+    s = torch.cuda.current_stream()
+    cp.decode(db.out, db.lse, ws, s)
+    torch.cuda.synchronize()
+    _check_oracle(db, bt)
+    ref_o, ref_l = db.out.clone(), db.lse.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        cp.decode(db.out, db.lse, ws, torch.cuda.current_stream())
+    _replay_and_compare(g, db, ref_o, ref_l, "cascade two streams")
+    cp.close()
+    pdattn.workspace_release(ws)
+
+
 def test_uniform_decode_attention_graph():
     bt = inputs.make_batch([2048, 100, 1], 16, 4, seed=33)
     db = DeviceBatch(bt)
