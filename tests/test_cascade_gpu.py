@@ -128,6 +128,14 @@ TREE_CASES = [
      [((0,), 10), ((0,), 20), ((1,), 5), ((1,), 300), ((), 77)], 32, 8, 2, 1),
     ("system prompt + 4 documents", [((0,), 1024)] + [((0, g), 512) for g in range(1, 5)],
      [((0, g), 64 + 17 * i) for g in range(1, 5) for i in range(4)], 32, 8, 5, 2),
+    ("G=8 two levels", [((0,), 128), ((0, 1), 256), ((0, 2), 64)],
+     [((0, 1), 9), ((0, 1), 100), ((0, 2), 33), ((0, 2), 1)], 32, 4, 3, 2),
+    ("G=2 three levels", [((0,), 64), ((0, 1), 64), ((0, 1, 2), 128)],
+     [((0, 1, 2), 5), ((0, 1, 2), 70), ((0, 1), 16), ((0,), 40)], 16, 8, 3, 3),
+    ("MHA (G=1) forest", [((0,), 160), ((1,), 96), ((1, 2), 48)],
+     [((0,), 3), ((0,), 200), ((1, 2), 7), ((1, 2), 31), ((1,), 12)], 8, 8, 3, 2),
+    ("root of 70 requests: two query groups", [((0,), 512), ((0, 1), 256)],
+     [((0, 1), 1 + i) for i in range(35)] + [((0,), 3 + i) for i in range(35)], 32, 8, 2, 2),
 ]
 
 
