@@ -225,10 +225,21 @@ def cpu_baseline(bt_lens, Hq, Hkv, seed, budget_s=10.0):
         if el >= budget_s or runs >= 200:
             break
     per = el / runs
+    # the reference's own oracle is single-threaded: one thread as well, on a bounded sample
+    runs1, t1 = 0, time.perf_counter()
+    while True:
+        oracle.decode(bt.q, bt.k, bt.v, bt.indptr, bt.indices, bt.last, Hq, Hkv, threads=1)
+        runs1 += 1
+        el1 = time.perf_counter() - t1
+        if el1 >= budget_s / 2 or runs1 >= 50:
+            break
+    per1 = el1 / runs1
     return {"value": round(bt.algorithmic_bytes() / per / 1e9, 3), "unit": "GB/s",
             "cores": threads, "kind": "port",
             "sample": f"full B={bt.B} L={bt_lens[0]} workload, fp64 oracle (oracle/pdattn_oracle.c) "
-                      f"x{runs} runs, {per * 1e3:.1f} ms/run on {threads} threads"}
+                      f"x{runs} runs, {per * 1e3:.1f} ms/run on {threads} threads",
+            "value_1_thread": round(bt.algorithmic_bytes() / per1 / 1e9, 3),
+            "sample_1_thread": f"same workload x{runs1} runs, {per1 * 1e3:.1f} ms/run on 1 thread"}
 
 
 def decode_workload(timer, lens, args, with_uniform):
@@ -285,8 +296,12 @@ def cascade_workload(timer, args):
     mn, mc, mo = statistics.median(w3n), statistics.median(w3c), statistics.median(w3o)
     cp.set_overlap(False)
     ci = cp.info()
+    from pdattn import inputs
+    ub, nb = inputs.unique_bytes(bt3), bt3.algorithmic_bytes()
     out = {"non_shared_us": round(mn * 1e3, 2), "cascade_us": round(mc * 1e3, 2),
            "speedup": round(mn / mc, 2), "cascade_two_streams_us": round(mo * 1e3, 2),
+           "unique_bytes": ub, "cascade_GB/s": round(gbs(ub, mc * 1e-3), 1),
+           "non_shared_bytes": nb, "non_shared_GB/s": round(gbs(nb, mn * 1e-3), 1),
            "prefix_chunks": ci.prefix_chunks,
            "prefix_workgroups": ci.prefix_workgroups, "suffix_workgroups": ci.suffix_workgroups}
     cp.close()
@@ -462,7 +477,9 @@ def tree_workload(timer, args):
         cp.close()
         pdattn.workspace_release(cws)
     del t, ws
-    return {"requests": 64, "non_shared_us": round(mn, 2), "single_level_us": round(m1, 2),
+    ub = inputs.unique_bytes(bt)
+    return {"requests": 64, "unique_bytes": ub, "tree_GB/s": round(gbs(ub, mt * 1e-6), 1),
+            "non_shared_us": round(mn, 2), "single_level_us": round(m1, 2),
             "tree_us": round(mt, 2), "tree_speedup_vs_non_shared": round(mn / mt, 2),
             "tree_speedup_vs_single_level": round(m1 / mt, 2), "tree_nodes": info.nodes,
             "tree_levels": info.levels}

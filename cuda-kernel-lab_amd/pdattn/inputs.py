@@ -63,6 +63,21 @@ class Batch:
         return kv + qo + lse + table
 
 
+def unique_bytes(bt) -> int:
+    """HBM bytes a step must move when every physical page is read once, however many sequences
+    share it (what a cascade can reach): the valid tokens of each distinct page, plus q, o, lse
+    and the page table."""
+    valid = {}
+    for b in range(bt.B):
+        pb, pe = int(bt.indptr[b]), int(bt.indptr[b + 1])
+        for j in range(pb, pe):
+            n = PAGE if j < pe - 1 else int(bt.last[b])
+            pid = int(bt.indices[j])
+            valid[pid] = max(valid.get(pid, 0), n)
+    kv = sum(valid.values()) * bt.Hkv * HEAD_DIM * 2 * 2
+    return kv + 2 * bt.B * bt.Hq * HEAD_DIM * 2 + bt.B * bt.Hq * 4 + 4 * (2 * bt.B + 1 + int(bt.indptr[-1]))
+
+
 def page_table(lens, rng: np.random.Generator):
     """CSR page table for the given lengths with a random permutation of physical pages
     (01_decode_attention.cu:343-354)."""

@@ -55,3 +55,14 @@ def test_prefix_tree_batch():
     assert sorted(set(flat)) == list(range(bt.num_pages))   # every page used, ids in range
     # each page is used by one sequence, or by the members of the one node that owns it
     assert bt.num_pages == 2 + 3 + 1 + (1 + 1 + 1 + 2)
+
+
+def test_unique_bytes():
+    """Shared pages count once; without sharing it equals the per-sequence algorithmic bytes."""
+    bt = inputs.make_shared_prefix_batch(64, [1, 17, 40], 8, 8, seed=13, fill=False)
+    tokens = 64 + 1 + 17 + 40
+    table = 4 * (2 * bt.B + 1 + int(bt.indptr[-1]))
+    assert inputs.unique_bytes(bt) == tokens * 8 * 512 + 2 * bt.B * 8 * 256 + bt.B * 8 * 4 + table
+    assert bt.algorithmic_bytes() - inputs.unique_bytes(bt) == 2 * 64 * 8 * 512   # two extra reads
+    plain = inputs.make_batch([5, 300, 17], 8, 2, seed=3, fill=False)
+    assert inputs.unique_bytes(plain) == plain.algorithmic_bytes()
