@@ -285,21 +285,24 @@ def cascade_workload(timer, args):
     cws = pdattn.Workspace()
     cp.decode(t3["out"], t3["lse"], cws, s)  # uploads the schedule
 
-    def f3c():
-        cp.set_overlap(False)    # every launch on the caller's stream (the default)
-        cp.decode(t3["out"], t3["lse"], cws, s)
+    default = cp.info().mode
 
-    def f3o():
-        cp.set_overlap(True)     # prefix launches forked onto the plan's second stream
-        cp.decode(t3["out"], t3["lse"], cws, s)
-    w3n, w3c, w3o = timer.run([f3n, f3c, f3o], args.steps, args.warmup, rounds=3)
-    mn, mc, mo = statistics.median(w3n), statistics.median(w3c), statistics.median(w3o)
-    cp.set_overlap(False)
+    def mode_fn(mode):
+        def f():
+            cp.set_mode(mode)
+            cp.decode(t3["out"], t3["lse"], cws, s)
+        return f
+    f3c, f3s, f3o = (mode_fn(m) for m in (default, pdattn.CASCADE_SERIAL, pdattn.CASCADE_TWO_STREAMS))
+    w3n, w3c, w3s, w3o = timer.run([f3n, f3c, f3s, f3o], args.steps, args.warmup, rounds=3)
+    mn, mc, ms, mo = (statistics.median(w) for w in (w3n, w3c, w3s, w3o))
+    cp.set_mode(default)
     ci = cp.info()
     from pdattn import inputs
     ub, nb = inputs.unique_bytes(bt3), bt3.algorithmic_bytes()
     out = {"non_shared_us": round(mn * 1e3, 2), "cascade_us": round(mc * 1e3, 2),
-           "speedup": round(mn / mc, 2), "cascade_two_streams_us": round(mo * 1e3, 2),
+           "speedup": round(mn / mc, 2),
+           "mode": {0: "fused", 1: "serial", 2: "two_streams"}[default],
+           "cascade_serial_us": round(ms * 1e3, 2), "cascade_two_streams_us": round(mo * 1e3, 2),
            "unique_bytes": ub, "cascade_GB/s": round(gbs(ub, mc * 1e-3), 1),
            "non_shared_bytes": nb, "non_shared_GB/s": round(gbs(nb, mn * 1e-3), 1),
            "prefix_chunks": ci.prefix_chunks,

@@ -62,6 +62,7 @@ struct DeviceFacts {
     int occ_partial[9] = {};
     int occ_balanced[9] = {};
     int occ_prefix[9] = {};
+    int occ_step[9] = {};
     char arch[64] = {};
 };
 
@@ -83,6 +84,7 @@ int device_facts(DeviceFacts* out) {
             f.occ_partial[G] = occupancy_decode_partial(G);
             f.occ_balanced[G] = occupancy_decode_balanced(G);
             f.occ_prefix[G] = occupancy_cascade_prefix(G);
+            f.occ_step[G] = occupancy_cascade_step(G);
         }
     }
     *out = f;
@@ -204,9 +206,9 @@ struct pdattn_cascade_plan {
     void* pinned = nullptr;
     size_t off_ppo = 0, off_pplse = 0, off_blob = 0, off_sk = 0, ws_bytes = 0;
     const void* uploaded_to = nullptr;
-    // prefix launches on a second stream, concurrent with the suffix decode (created on first
-    // use); off by default: on MI355X the fork / join events cost more than the overlap recovers
-    int overlap = 0;
+    // how the prefix and suffix passes run (pdattn_cascade_set_mode); the second stream of the
+    // two-stream mode is created on first use
+    int mode = PDATTN_CASCADE_SERIAL;
     hipStream_t aux = nullptr;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
 };
@@ -380,13 +382,35 @@ int upload_plan(pdattn_plan* pl, void* ws, size_t bytes, hipStream_t s) {
     return PDATTN_OK;
 }
 
+// The argument block of a plan's decode launch (its workspace already checked).
+BalArgs bal_args(const pdattn_plan* pl, const void* q, const void* k, const void* v,
+                 const int32_t* indices, float sm_scale, void* out, float* lse, char* base) {
+    BalArgs a;
+    a.q = static_cast<const _Float16*>(q);
+    a.k = static_cast<const uint8_t*>(k);
+    a.v = static_cast<const uint8_t*>(v);
+    a.kv_indices = indices + pl->jbase;
+    a.out = static_cast<_Float16*>(out);
+    a.lse = lse;
+    a.desc = reinterpret_cast<const int32_t*>(base + pl->off_desc);
+    a.part_o = reinterpret_cast<float*>(base + pl->off_po);
+    a.part_lse = reinterpret_cast<float*>(base + pl->off_plse);
+    a.B = pl->B;
+    a.Hq = pl->Hq;
+    a.Hkv = pl->Hkv;
+    a.W = pl->W;
+    a.scale_log2 = sm_scale * 1.4426950408889634f;
+    return a;
+}
+
 // Balanced decode launch, then (when the plan lists any) the merge launch. With `join`, the
 // stream waits for that event between the two (the extra partials come from another stream).
+// decode = false: the decode workgroups ran elsewhere (the fused cascade step); merge only.
 int run_plan(const pdattn_plan* pl, const void* q, const void* k, const void* v,
              const int32_t* indptr, const int32_t* indices, const int32_t* last, float sm_scale,
              void* out, float* lse, void* ws, size_t bytes, hipStream_t s,
              const float* extra_o = nullptr, const float* extra_lse = nullptr, int n_extra = 0,
-             hipEvent_t join = nullptr) {
+             hipEvent_t join = nullptr, bool decode = true) {
     if (ws != pl->uploaded_to)
         return fail(PDATTN_ERR_NOT_READY, "plan was not uploaded into this workspace");
     if (bytes < pl->ws_bytes)
@@ -400,24 +424,8 @@ int run_plan(const pdattn_plan* pl, const void* q, const void* k, const void* v,
     char* base = static_cast<char*>(ws);
     float* part_lse = reinterpret_cast<float*>(base + pl->off_plse);
     float* part_o = reinterpret_cast<float*>(base + pl->off_po);
-    if (pl->U > 0) {
-        BalArgs a;
-        a.q = static_cast<const _Float16*>(q);
-        a.k = static_cast<const uint8_t*>(k);
-        a.v = static_cast<const uint8_t*>(v);
-        a.kv_indices = indices + pl->jbase;
-        a.out = static_cast<_Float16*>(out);
-        a.lse = lse;
-        a.desc = reinterpret_cast<const int32_t*>(base + pl->off_desc);
-        a.part_o = part_o;
-        a.part_lse = part_lse;
-        a.B = pl->B;
-        a.Hq = pl->Hq;
-        a.Hkv = pl->Hkv;
-        a.W = pl->W;
-        a.scale_log2 = sm_scale * 1.4426950408889634f;
-        PD_HIP(launch_decode_balanced(a, pl->G, s));
-    }
+    if (pl->U > 0 && decode)
+        PD_HIP(launch_decode_balanced(bal_args(pl, q, k, v, indices, sm_scale, out, lse, base), pl->G, s));
     if (join) PD_HIP(hipStreamWaitEvent(s, join, 0));
     if (pl->n_entries) {
         MergeArgs m;
@@ -552,30 +560,38 @@ int cascade_plan_create(const pdattn_decode_params* base, const int32_t* h_indpt
         cp->off_sk = 0;
         cp->ws_bytes = cp->sk.ws_bytes;
     } else {
-        // One prefix launch per depth (its nodes have disjoint members), sized to fill about one
-        // wave of prefix workgroups: chunk tokens ctok (a multiple of 64 in [256, 8192]) such that
-        // sum over the depth's nodes of query groups x Hkv x ceil(tokens / ctok) ~ the target.
-        // Partial columns: one range per depth, as wide as its node with the most chunks.
-        const int target = f.cus * std::max(1, f.occ_prefix[G]);
+        // compacted suffix page table: pages start[b].. of every sequence
+        std::vector<int32_t> sind(B + 1, 0);
+        std::vector<int32_t> sidx;
+        for (int b = 0; b < B; ++b) {
+            for (int i = h_indptr[b] + start[b]; i < h_indptr[b + 1]; ++i) sidx.push_back(h_indices[i]);
+            sind[b + 1] = (int32_t)sidx.size();
+        }
+        st = build_balanced_plan(sind.data(), last.data(), B, base->Hq, base->Hkv, 0, 0, true, &cp->sk);
+        // The prefix work of every node goes into one launch (nodes of different depths write
+        // different partial columns, so they are independent). Fused step (default where two of
+        // its workgroups fit on a CU): about one prefix workgroup per CU, beside the suffix
+        // decode's one. Separate prefix launch: enough workgroups to fill every CU slot. Chunk
+        // tokens ctok (a multiple of 64 in [256, 8192]) such that the sum over nodes of query
+        // groups x Hkv x ceil(tokens / ctok) is about that target. Partial columns: one range per
+        // depth, as wide as its node with the most chunks.
+        cp->mode = f.occ_step[G] >= 2 ? PDATTN_CASCADE_FUSED : PDATTN_CASCADE_SERIAL;
+        const int target = cp->mode == PDATTN_CASCADE_FUSED ? f.cus : f.cus * std::max(1, f.occ_prefix[G]);
         int depths = 0;
         for (const CascadeNode& n : cp->nodes) depths = std::max(depths, n.depth + 1);
         std::vector<int> depth_cols(depths, 0);
-        for (int d = 0; d < depths; ++d) {
-            double units = 0;
-            for (CascadeNode& n : cp->nodes) {
-                if (n.depth != d) continue;
-                n.qgroups = (n.ns * G + prefix_rows_per_workgroup() - 1) / prefix_rows_per_workgroup();
-                units += (double)n.qgroups * base->Hkv * (n.p1 - n.p0) * kPage;
-            }
-            int ctok = (int)(units / target);
-            ctok = std::min(std::max((ctok + 63) / 64 * 64, 256), 8192);
-            for (CascadeNode& n : cp->nodes) {
-                if (n.depth != d) continue;
-                const int Lp = (n.p1 - n.p0) * kPage;
-                n.ctok = std::min(ctok, (Lp + 63) / 64 * 64);
-                n.nchunks = (Lp + n.ctok - 1) / n.ctok;
-                depth_cols[d] = std::max(depth_cols[d], n.nchunks);
-            }
+        double units = 0;
+        for (CascadeNode& n : cp->nodes) {
+            n.qgroups = (n.ns * G + prefix_rows_per_workgroup() - 1) / prefix_rows_per_workgroup();
+            units += (double)n.qgroups * base->Hkv * (n.p1 - n.p0) * kPage;
+        }
+        int ctok = (int)(units / target);
+        ctok = std::min(std::max((ctok + 63) / 64 * 64, 256), 8192);
+        for (CascadeNode& n : cp->nodes) {
+            const int Lp = (n.p1 - n.p0) * kPage;
+            n.ctok = std::min(ctok, (Lp + 63) / 64 * 64);
+            n.nchunks = (Lp + n.ctok - 1) / n.ctok;
+            depth_cols[n.depth] = std::max(depth_cols[n.depth], n.nchunks);
         }
         std::vector<int> col_of_depth(depths + 1, 0);
         for (int d = 0; d < depths; ++d) col_of_depth[d + 1] = col_of_depth[d] + depth_cols[d];
@@ -583,7 +599,7 @@ int cascade_plan_create(const pdattn_decode_params* base, const int32_t* h_indpt
         cp->n_extra = col_of_depth.back();
         cp->levels = depths;
         cp->Lp = (cp->nodes[0].p1 - cp->nodes[0].p0) * kPage;
-        // per-depth item lists (items of depth 0 first), each item carrying its node's fields
+        // the item list (items of depth 0 first), each item carrying its node's fields
         std::vector<int32_t> items;
         cp->level_items.assign(depths, 0);
         for (int d = 0; d < depths; ++d)
@@ -598,14 +614,6 @@ int cascade_plan_create(const pdattn_decode_params* base, const int32_t* h_indpt
                     }
             }
         cp->n_items = (int)(items.size() / 8);
-        // compacted suffix page table: pages start[b].. of every sequence
-        std::vector<int32_t> sind(B + 1, 0);
-        std::vector<int32_t> sidx;
-        for (int b = 0; b < B; ++b) {
-            for (int i = h_indptr[b] + start[b]; i < h_indptr[b + 1]; ++i) sidx.push_back(h_indices[i]);
-            sind[b + 1] = (int32_t)sidx.size();
-        }
-        st = build_balanced_plan(sind.data(), last.data(), B, base->Hq, base->Hkv, 0, 0, true, &cp->sk);
         cp->n_suffix_idx = (int)sidx.size();
         cp->blob = sind;
         cp->blob.insert(cp->blob.end(), sidx.begin(), sidx.end());
@@ -900,6 +908,7 @@ int pdattn_cascade_plan_get_info(const pdattn_cascade_plan* cp, pdattn_cascade_i
     info->workspace_bytes = cp->ws_bytes;
     info->nodes = (int)cp->nodes.size();
     info->levels = cp->levels;
+    info->mode = cp->mode;
     return PDATTN_OK;
 }
 
@@ -937,11 +946,46 @@ int pdattn_cascade_decode(pdattn_cascade_plan* cp, void* out, float* lse, pdattn
     const int32_t* sidx = sind + (p.B + 1);
     const int32_t* dseqs = sidx + cp->n_suffix_idx;
     const int32_t* ditems = dseqs + cp->n_seqs;
-    // One prefix launch per depth of the tree (a depth's nodes have disjoint members). With overlap
-    // the prefix launches run on the plan's second stream while the suffix decode runs on `s`;
-    // `s` waits for them before the merge, so the step stays one fork / join (graph-capturable).
+    // the prefix pass over every node's items (one workgroup per item and kv head)
+    PrefixArgs a;
+    a.q = static_cast<const _Float16*>(p.q);
+    a.k = static_cast<const uint8_t*>(p.k_cache);
+    a.v = static_cast<const uint8_t*>(p.v_cache);
+    a.prefix_pages = cp->d_indices;
+    a.seqs = dseqs;
+    a.items = ditems;
+    a.part_o = ppo;
+    a.part_lse = pplse;
+    a.B = p.B;
+    a.Hq = p.Hq;
+    a.Hkv = p.Hkv;
+    a.prefix_len = 0;
+    a.chunk_tokens = 0;
+    a.part_stride = cp->n_extra;
+    a.num_chunks = cp->n_items;
+    a.ns = 0;
+    a.col0 = 0;
+    a.scale_log2 = p.sm_scale * 1.4426950408889634f;
+    char* skb = base + cp->off_sk;
+    if (cp->mode == PDATTN_CASCADE_FUSED) {
+        // one launch: the suffix decode's workgroups, then the prefix workgroups beside them
+        if (cp->sk.ws_bytes > 0 && skb != cp->sk.uploaded_to)
+            return fail(PDATTN_ERR_NOT_READY, "suffix plan was not uploaded into this workspace");
+        StepArgs sa;
+        sa.d = bal_args(&cp->sk, p.q, p.k_cache, p.v_cache, sidx, p.sm_scale, out, lse, skb);
+        sa.p = a;
+        sa.n_dec = cp->sk.U > 0 ? cp->sk.W : 0;
+        sa.n_pre = cp->n_items * p.Hkv;
+        PD_HIP(launch_cascade_step(sa, p.Hq / p.Hkv, s));
+        return run_plan(&cp->sk, p.q, p.k_cache, p.v_cache, sind, sidx, p.kv_last_page_len, p.sm_scale,
+                        out, lse, skb, cp->sk.ws_bytes, s, ppo, pplse, cp->n_extra, nullptr, false);
+    }
+    // Separate launches. Two streams: the prefix launch runs on the plan's second stream while
+    // the suffix decode runs on `s`; `s` waits for it before the merge, so the step stays one
+    // fork / join (graph-capturable).
+    const bool two = cp->mode == PDATTN_CASCADE_TWO_STREAMS;
     hipStream_t ps = s;
-    if (cp->overlap) {
+    if (two) {
         if (!cp->aux) {
             PD_HIP(hipStreamCreateWithFlags(&cp->aux, hipStreamNonBlocking));
             PD_HIP(hipEventCreateWithFlags(&cp->ev_fork, hipEventDisableTiming));
@@ -951,39 +995,25 @@ int pdattn_cascade_decode(pdattn_cascade_plan* cp, void* out, float* lse, pdattn
         PD_HIP(hipStreamWaitEvent(cp->aux, cp->ev_fork, 0));
         ps = cp->aux;
     }
-    int item0 = 0;
-    for (int d = 0; d < cp->levels; ++d) {
-        PrefixArgs a;
-        a.q = static_cast<const _Float16*>(p.q);
-        a.k = static_cast<const uint8_t*>(p.k_cache);
-        a.v = static_cast<const uint8_t*>(p.v_cache);
-        a.prefix_pages = cp->d_indices;
-        a.seqs = dseqs;
-        a.items = ditems + 8 * (size_t)item0;
-        a.part_o = ppo;
-        a.part_lse = pplse;
-        a.B = p.B;
-        a.Hq = p.Hq;
-        a.Hkv = p.Hkv;
-        a.prefix_len = 0;
-        a.chunk_tokens = 0;
-        a.part_stride = cp->n_extra;
-        a.num_chunks = cp->level_items[d];
-        a.ns = 0;
-        a.col0 = 0;
-        a.scale_log2 = p.sm_scale * 1.4426950408889634f;
-        PD_HIP(launch_cascade_prefix(a, p.Hq / p.Hkv, 1, ps));
-        item0 += cp->level_items[d];
-    }
-    if (cp->overlap) PD_HIP(hipEventRecord(cp->ev_join, ps));
+    PD_HIP(launch_cascade_prefix(a, p.Hq / p.Hkv, 1, ps));
+    if (two) PD_HIP(hipEventRecord(cp->ev_join, ps));
     return run_plan(&cp->sk, p.q, p.k_cache, p.v_cache, sind, sidx, p.kv_last_page_len, p.sm_scale,
-                    out, lse, base + cp->off_sk, cp->sk.ws_bytes, s, ppo, pplse, cp->n_extra,
-                    cp->overlap ? cp->ev_join : nullptr);
+                    out, lse, skb, cp->sk.ws_bytes, s, ppo, pplse, cp->n_extra,
+                    two ? cp->ev_join : nullptr);
 }
 
-int pdattn_cascade_set_overlap(pdattn_cascade_plan* cp, int enable) {
+int pdattn_cascade_set_mode(pdattn_cascade_plan* cp, int mode) {
     if (!cp) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null plan");
-    cp->overlap = enable ? 1 : 0;
+    if (mode != PDATTN_CASCADE_FUSED && mode != PDATTN_CASCADE_SERIAL && mode != PDATTN_CASCADE_TWO_STREAMS)
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "unknown cascade mode %d", mode);
+    if (mode == PDATTN_CASCADE_FUSED) {
+        DeviceFacts f;
+        if (int st = device_facts(&f)) return st;
+        const int G = cp->base.Hkv > 0 ? cp->base.Hq / cp->base.Hkv : 1;
+        if (G < 1 || G > 8 || f.occ_step[G] < 2)
+            return fail(PDATTN_ERR_UNSUPPORTED, "the fused cascade step does not fit two workgroups per CU at G=%d", G);
+    }
+    cp->mode = mode;
     return PDATTN_OK;
 }
 

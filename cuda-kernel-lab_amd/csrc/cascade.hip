@@ -1,296 +1,20 @@
-// cascade.hip -- shared-prefix ("cascade") attention on CDNA4 fp16 MFMA.
-//
-// With prefix caching, all B sequences of a batch start with the same physical pages. Their
-// B*G query rows per kv head (G = Hq/Hkv) are stacked into one matrix and attend to the shared
-// keys once, as a dense contraction (qilem/cuda-kernel-lab, 01_decode_attention.cu:446-632 does
-// the same with WMMA in two passes). Here it is a single pass with an online softmax:
-//
-//   S^T = K Q^T   (v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims, B = 32 dims x 16 queries)
-//   O^T += V^T P^T (A = 16 dims x 32 keys, B = 32 keys x 16 queries)
-//
-// Computing the transposed products puts one query per lane column of every 16x16 accumulator
-// (lane l holds rows 4*(l/16)+j, column l%16), so
-//   * the running max / sum of a query live in the lanes of that column: a row max over a key
-//     tile is an in-lane max plus two cross-lane steps, and the rescale of the output
-//     accumulator by exp(m_old - m_new) is a per-lane scalar multiply;
-//   * P leaves the S^T accumulator already in the B-operand layout of the PV product (the 8
-//     keys a lane contributes are 4 of one 16-key tile and 4 of the next; V^T is read with the
-//     same key order), so P needs no cross-lane movement.
-// K is staged in LDS as [key][16-byte chunk] with the chunk index XOR-ed by (key & 15): the
-// A-operand reads (16 keys x one chunk per 16-lane phase) hit 16 distinct bank groups. V is
-// staged transposed (V^T[dim][key pair], rows padded to 33 dwords) so that the A operand of the
-// PV product is two conflict-free 8-byte reads. Two LDS buffers: the global loads of block n+1
-// are in flight while block n is computed.
-//
-// A workgroup: 8 waves x 2 query tiles x 16 = 256 stacked query rows of one kv head, one chunk
-// of prefix keys, written as the normalized partial (o, lse) of that chunk. The query rows are
-// those of the sequences that share the prefix (all B, or a listed subset for one node of a
-// prefix tree); chunk c of the prefix writes partial column col0 + c of each of their rows. Two
-// waves per SIMD: one wave's softmax (VALU) runs while the other's products occupy the matrix
-// core, and the per-wave register budget (~200) keeps the accumulators out of AGPRs, so the
-// softmax rescale touches them in place.
-#include <math.h>
-
-#include "pdattn_internal.h"
+// cascade.hip -- the prefix kernel of the shared-prefix (cascade) path: one workgroup per
+// (prefix chunk or tree item, query group, kv head), the body in prefix_body.h.
+#include "prefix_body.h"
 
 namespace pdattn {
 namespace {
 
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-constexpr float kLn2 = 0.69314718055994531f;
-constexpr int PW = 8;               // waves per workgroup
-constexpr int PT = PW * 64;         // threads per workgroup
-constexpr int QT = 2;               // 16-query tiles per wave
-constexpr int QROWS = PW * QT * 16; // stacked query rows per workgroup
-constexpr int KB = 64;              // keys per LDS block
-constexpr int VTS = 33;             // V^T row stride in dwords (32 key pairs + 1 pad)
-constexpr int MAXPG = 512;          // pages per chunk, i.e. chunk_tokens <= 8192
-
-struct PSmem {
-    u32x4 K[2][KB][16];              // [key][chunk ^ (key & 15)], 16 bytes = 8 dims per chunk
-    uint32_t VT[2][kHeadDim][VTS];   // [dim][key pair]: low half key 2p, high half key 2p+1
-    int pg[MAXPG];                   // physical pages of this chunk
-    int sq[QROWS];                   // sequences of this group's query rows (one per G rows)
-};
-
-__device__ __forceinline__ f32x4 mfma16x16x32(const f16x8& a, const f16x8& b, const f32x4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-// The work of one workgroup with NT query tiles per wave. Query tile tq of a wave is tile
-// tq * PW + wave of the workgroup's rows, so a group of up to 16 * PW * NT rows occupies the first
-// NT tiles of every wave.
-template <int NT>
-__device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int chunk, int qgrp,
-                                             int kvh) {
-    const int G = a.Hq / a.Hkv, nq = a.ns * G;
-    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-    const int l16 = lane & 15, lg = lane >> 4;
-    const int kbeg = chunk * a.chunk_tokens;
-    const int kend = min(a.prefix_len, kbeg + a.chunk_tokens);
-    const int nkeys = max(0, kend - kbeg);
-    const int npg = (nkeys + kPage - 1) / kPage;
-    const int nblk = (nkeys + KB - 1) / KB;
-    const size_t page_bytes = (size_t)kPage * a.Hkv * 256;
-    const int s0 = qgrp * (QROWS / G);                 // first member of this query group
-    const int nsq = min(QROWS / G, a.ns - s0);
-
-    // page ids and member ids in one round trip
-    for (int i = tid; i < npg; i += PT) sm.pg[i] = a.prefix_pages[kbeg / kPage + i];
-    for (int j = tid; j < nsq; j += PT) sm.sq[j] = a.seqs ? a.seqs[s0 + j] : s0 + j;
-
-    // Staging: thread t moves 16-byte chunk sc = t & 15 of K rows sr and sr + 32 and of the V key
-    // pair (2 sr, 2 sr + 1), sr = t >> 4. Keys past the chunk read the last valid key instead (a
-    // real, finite row): their scores are masked to -inf below, so their weights are exactly 0.
-    const int sc = tid & 15, sr = tid >> 4;
-    u32x4 kst[2], vst[2];
-    auto gload = [&](int kb) {
-        const int key0 = kbeg + kb * KB;
-        int key[4] = {key0 + sr, key0 + sr + 32, key0 + 2 * sr, key0 + 2 * sr + 1};
-        uint32_t pid[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            key[i] = min(key[i], kend - 1);
-            pid[i] = (uint32_t)sm.pg[(key[i] - kbeg) >> 4];
-        }
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-            kst[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-                a.k + pid[i] * page_bytes + (size_t)(((key[i] & 15) * a.Hkv + kvh) * 256 + sc * 16)));
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-            vst[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-                a.v + pid[2 + i] * page_bytes + (size_t)(((key[2 + i] & 15) * a.Hkv + kvh) * 256 + sc * 16)));
-    };
-    auto lstore = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int n = sr + 32 * i;
-            sm.K[buf][n][sc ^ (n & 15)] = kst[i];
-        }
-        const u32x4 lo = vst[0], hi = vst[1];   // keys 2 sr and 2 sr + 1, dims 8 sc .. +7
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            sm.VT[buf][8 * sc + 2 * e][sr] = __builtin_amdgcn_perm(hi[e], lo[e], 0x05040100u);
-            sm.VT[buf][8 * sc + 2 * e + 1][sr] = __builtin_amdgcn_perm(hi[e], lo[e], 0x07060302u);
-        }
-    };
-
-    __syncthreads();   // page ids, member ids
-    if (nblk > 0) gload(0);
-
-    // B operands of S^T: Q[query][32 ks + 8 lg .. +7], query = l16 of tile tq; loaded behind the
-    // first block (rows past the group read its last row and are zeroed)
-    f16x8 qb[NT][4];
-    int qrow[NT];
-#pragma unroll
-    for (int tq = 0; tq < NT; ++tq) {
-        const int r = (tq * PW + wave) * 16 + l16;    // row within the group
-        const bool ok = qgrp * QROWS + r < nq;
-        const int rr = ok ? r : nsq * G - 1;
-        const int b = sm.sq[rr / G], g = rr % G;
-        const _Float16* qp = a.q + ((size_t)b * a.Hq + kvh * G + g) * kHeadDim + 8 * lg;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) qb[tq][ks] = *reinterpret_cast<const f16x8*>(qp + 32 * ks);
-        qrow[tq] = ok ? b * a.Hq + kvh * G + g : -1;
-    }
-#pragma unroll
-    for (int tq = 0; tq < NT; ++tq)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-            if (qrow[tq] < 0) qb[tq][ks] = f16x8{};
-
-    f32x4 acc[NT][8];
-    float m_run[NT], l_run[NT];
-#pragma unroll
-    for (int tq = 0; tq < NT; ++tq) {
-        m_run[tq] = -INFINITY;
-        l_run[tq] = 0.f;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) acc[tq][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-
-    if (nblk > 0) lstore(0);
-    __syncthreads();
-
-    for (int kb = 0; kb < nblk; ++kb) {
-        const int buf = kb & 1;
-        const bool more = kb + 1 < nblk;
-        if (more) gload(kb + 1);
-
-        // S^T tiles: s[tq][tk][j] = score(key 16 tk + 4 lg + j, query l16 of tile tq)
-        f32x4 s[NT][4];
-#pragma unroll
-        for (int tk = 0; tk < 4; ++tk) {
-            f16x8 ka[4];
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
-                ka[ks] = __builtin_bit_cast(f16x8, sm.K[buf][16 * tk + l16][(4 * ks + lg) ^ l16]);
-#pragma unroll
-            for (int tq = 0; tq < NT; ++tq) {
-                f32x4 c = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks) c = mfma16x16x32(ka[ks], qb[tq][ks], c);
-                s[tq][tk] = c;
-            }
-        }
-
-        // online softmax (base 2) per query
-        const int kbase = kbeg + kb * KB + 4 * lg;
-        float mn[NT];
-        bool grow = false;
-#pragma unroll
-        for (int tq = 0; tq < NT; ++tq) {
-            float mx = -INFINITY;
-#pragma unroll
-            for (int tk = 0; tk < 4; ++tk)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const bool ok = kbase + 16 * tk + j < kend;
-                    const float x = ok ? s[tq][tk][j] * a.scale_log2 : -INFINITY;
-                    s[tq][tk][j] = x;
-                    mx = fmaxf(mx, x);
-                }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            mn[tq] = fmaxf(m_run[tq], mx);
-            grow |= mn[tq] > m_run[tq];
-        }
-        if (__builtin_amdgcn_ballot_w64(grow)) {
-#pragma unroll
-            for (int tq = 0; tq < NT; ++tq) {
-                const float al = (mn[tq] > m_run[tq]) ? __builtin_amdgcn_exp2f(m_run[tq] - mn[tq]) : 1.f;
-                l_run[tq] *= al;
-#pragma unroll
-                for (int dt = 0; dt < 8; ++dt) acc[tq][dt] *= al;
-                m_run[tq] = mn[tq];
-            }
-        }
-        f16x8 pb[NT][2];
-#pragma unroll
-        for (int tq = 0; tq < NT; ++tq) {
-            const float ms = (m_run[tq] == -INFINITY) ? 0.f : m_run[tq];
-#pragma unroll
-            for (int tk = 0; tk < 4; ++tk)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float p = __builtin_amdgcn_exp2f(s[tq][tk][j] - ms);
-                    l_run[tq] += p;   // fp32 weights for the denominator (exact lse); PV uses
-                    pb[tq][tk >> 1][(tk & 1) * 4 + j] = (_Float16)p;   // them rounded to nearest
-                }
-        }
-
-        // O^T += V^T P^T
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-            const int d = 16 * dt + l16;
-#pragma unroll
-            for (int kb2 = 0; kb2 < 2; ++kb2) {
-                const int p0 = 16 * kb2 + 2 * lg;
-                u32x4 raw;
-                raw[0] = sm.VT[buf][d][p0];
-                raw[1] = sm.VT[buf][d][p0 + 1];
-                raw[2] = sm.VT[buf][d][p0 + 8];
-                raw[3] = sm.VT[buf][d][p0 + 9];
-                const f16x8 va = __builtin_bit_cast(f16x8, raw);
-#pragma unroll
-                for (int tq = 0; tq < NT; ++tq) acc[tq][dt] = mfma16x16x32(va, pb[tq][kb2], acc[tq][dt]);
-            }
-        }
-
-        if (more) lstore(buf ^ 1);
-        __syncthreads();
-    }
-
-    // normalized partial of this chunk
-#pragma unroll
-    for (int tq = 0; tq < NT; ++tq) {
-        float L = l_run[tq];
-        L += __shfl_xor(L, 16);
-        L += __shfl_xor(L, 32);
-        if (qrow[tq] < 0) continue;
-        const size_t slot = (size_t)qrow[tq] * a.part_stride + a.col0 + chunk;
-        const float inv = L > 0.f ? 1.f / L : 0.f;
-        float* po = a.part_o + slot * kHeadDim + 4 * lg;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(po + 16 * dt) = acc[tq][dt] * inv;
-        if (lg == 0)
-            a.part_lse[slot] = L > 0.f ? (m_run[tq] + __builtin_amdgcn_logf(L)) * kLn2 : -INFINITY;
-    }
-}
-
-__global__ __launch_bounds__(PT) void cascade_prefix_kernel(PrefixArgs a) {
+// Two workgroups per CU (two waves per SIMD): one wave's softmax runs while the other's MFMAs
+// occupy the matrix core.
+__global__ __launch_bounds__(kPrefixThreads, 2) void cascade_prefix_kernel(PrefixArgs a) {
     __shared__ PSmem sm;
-    int chunk = blockIdx.x, qgrp = blockIdx.y;
-    const int kvh = blockIdx.z;
-    if (a.items) {
-        // one item of a multi-prefix launch: {page-table position of the node's first page,
-        // offset of its members in seqs, members, tokens, chunk tokens, first partial column,
-        // chunk, query group}
-        const int32_t* it = a.items + 8 * (size_t)blockIdx.x;
-        a.prefix_pages += it[0];
-        a.seqs += it[1];
-        a.ns = it[2];
-        a.prefix_len = it[3];
-        a.chunk_tokens = it[4];
-        a.col0 = it[5];
-        chunk = it[6];
-        qgrp = it[7];
-    }
-    // query tiles per wave that hold rows of this group (the same for the whole workgroup)
-    const int rows = a.ns * (a.Hq / a.Hkv) - qgrp * QROWS;
-    if (rows > 16 * PW)
-        prefix_chunk<QT>(a, sm, chunk, qgrp, kvh);
-    else
-        prefix_chunk<1>(a, sm, chunk, qgrp, kvh);
+    prefix_workgroup(a, sm, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 }  // namespace
 
-int prefix_rows_per_workgroup() { return QROWS; }
+int prefix_rows_per_workgroup() { return kPrefixRows; }
 
 hipError_t launch_cascade_prefix(const PrefixArgs& a, int G, int qtiles, hipStream_t s) {
     (void)G;
@@ -298,19 +22,19 @@ hipError_t launch_cascade_prefix(const PrefixArgs& a, int G, int qtiles, hipStre
     if (a.items) {
         // num_chunks = number of items
         if (a.num_chunks <= 0) return hipSuccess;
-        cascade_prefix_kernel<<<dim3(a.num_chunks, 1, a.Hkv), PT, 0, s>>>(a);
+        cascade_prefix_kernel<<<dim3(a.num_chunks, 1, a.Hkv), kPrefixThreads, 0, s>>>(a);
         return hipGetLastError();
     }
     if (a.num_chunks <= 0 || qtiles <= 0) return hipSuccess;
     dim3 grid(a.num_chunks, qtiles, a.Hkv);
-    cascade_prefix_kernel<<<grid, PT, 0, s>>>(a);
+    cascade_prefix_kernel<<<grid, kPrefixThreads, 0, s>>>(a);
     return hipGetLastError();
 }
 
 int occupancy_cascade_prefix(int G) {
     (void)G;
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&cascade_prefix_kernel), PT, 0) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(&cascade_prefix_kernel), kPrefixThreads, 0) != hipSuccess)
         return 1;
     return n > 0 ? n : 1;
 }

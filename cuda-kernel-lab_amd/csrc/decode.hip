@@ -36,6 +36,7 @@
 #include <cstdlib>
 
 #include "pdattn_internal.h"
+#include "prefix_body.h"
 
 namespace pdattn {
 namespace {
@@ -667,20 +668,30 @@ __device__ __forceinline__ void flush_segment(BalSmem<C::G, C::NW * C::RPI>& sm,
 // while a segment is flushed. Partials are written with plain stores and merged by a second
 // kernel, so no workgroup waits for another.
 template <class C>
-__global__ __launch_bounds__(C::NT) void decode_balanced_kernel(BalArgs a) {
+struct BalShared {
+    BalSmem<C::G, C::NW * C::RPI> sm;
+    int pg[kRangeMax];                             // the workgroup's page ids
+    u32x4 qs[kSegMax][C::G * kHeadDim / 8];        // q rows of each segment
+    int sd[kSegMax * kSegInts];                    // segment descriptors
+};
+
+// The body of one balanced-decode workgroup w (the kernel's argument block must start with the
+// BalArgs `a`, which kargs() reads).
+template <class C>
+__device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C>& S, int w) {
     constexpr int G = C::G, NW = C::NW, NT = C::NT, NBUF = C::NBUF, LPR = C::LPR;
-    __shared__ BalSmem<G, NW * C::RPI> sm;
-    __shared__ int pg[kRangeMax];
-    __shared__ u32x4 qs[kSegMax][G * kHeadDim / 8];
+    auto& sm = S.sm;
+    int* pg = S.pg;
+    auto& qs = S.qs;
+    int* sd = S.sd;
     // the wave index is made wave-uniform explicitly: everything the page ring derives from it
     // (per-wave page counts, page ids, buffer resources) must live in scalar registers
-    const int w = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane / LPR, c = lane % LPR;
     // Segment fields are staged in LDS and read back wave-uniform: global (vector) loads of them
     // would count against the same wait counter as the ring's page loads, and a non-uniform value
     // in a buffer resource would turn every page load into a loop over lanes.
-    __shared__ int sd[kSegMax * kSegInts];
     auto fld = [&](int si, int f) { return __builtin_amdgcn_readfirstlane(sd[si * kSegInts + f]); };
     const int32_t* desc = kargs()->desc + (size_t)w * kBalDescInts;
     const int nseg = __builtin_amdgcn_readfirstlane(desc[0]);
@@ -792,6 +803,32 @@ __global__ __launch_bounds__(C::NT) void decode_balanced_kernel(BalArgs a) {
     }
 }
 
+template <class C>
+__global__ __launch_bounds__(C::NT) void decode_balanced_kernel(BalArgs a) {
+    __shared__ BalShared<C> S;
+    balanced_body<C>(a, S, blockIdx.x);
+}
+
+// The fused cascade step: blocks [0, n_dec) are the suffix decode's workgroups, the rest the
+// prefix pass's (item x, kv head) workgroups. Both roles are 4-wave workgroups of about 210
+// VGPRs and 69 KB of LDS, so a CU holds one of each: the dispatcher places the first n_dec blocks
+// one per CU, and the prefix blocks fill the second slots, so every CU streams suffix pages
+// while its matrix core works on the prefix. Partials of both go to the workspace and are merged
+// by the next launch.
+template <class C>
+__global__ __launch_bounds__(C::NT, 2) void cascade_step_kernel(StepArgs s) {
+    static_assert(C::NT == kPrefixThreads, "both roles use the same workgroup shape");
+    constexpr size_t SB = sizeof(BalShared<C>) > sizeof(PSmem) ? sizeof(BalShared<C>) : sizeof(PSmem);
+    __shared__ __align__(16) unsigned char raw[SB];
+    const int i = blockIdx.x;
+    if (i < s.n_dec) {
+        balanced_body<C>(s.d, *reinterpret_cast<BalShared<C>*>(raw), i);
+    } else {
+        const int j = i - s.n_dec, n_items = s.p.num_chunks;
+        prefix_workgroup(s.p, *reinterpret_cast<PSmem*>(raw), j % n_items, 0, j / n_items);
+    }
+}
+
 int occupancy_of(const void* fn, int threads) {
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, 0) != hipSuccess) return 1;
@@ -819,6 +856,12 @@ template <class C>
 void launch_b(const BalArgs& a, hipStream_t s) {
     decode_balanced_kernel<C><<<a.W, C::NT, 0, s>>>(a);
 }
+template <class C>
+void launch_step(const StepArgs& a, hipStream_t s) {
+    cascade_step_kernel<C><<<a.n_dec + a.n_pre, C::NT, 0, s>>>(a);
+}
+template <class C>
+int occ_step() { return occupancy_of(reinterpret_cast<const void*>(&cascade_step_kernel<C>), C::NT); }
 template <class C>
 int occ_p() { return occupancy_of(reinterpret_cast<const void*>(&decode_partial_kernel<C>), C::NT); }
 template <class C>
@@ -860,6 +903,15 @@ hipError_t launch_decode_balanced(const BalArgs& a, int G, hipStream_t s) {
     PD_DISPATCH(BalCfg, G, launch_b, a, s);
     return hipGetLastError();
 }
+
+hipError_t launch_cascade_step(const StepArgs& a, int G, hipStream_t s) {
+    if (G != 1 && G != 2 && G != 4 && G != 8) return hipErrorInvalidValue;
+    if (a.n_dec + a.n_pre <= 0) return hipSuccess;
+    PD_DISPATCH(BalCfg, G, launch_step, a, s);
+    return hipGetLastError();
+}
+
+int occupancy_cascade_step(int G) { PD_DISPATCH_RET(BalCfg, G, occ_step); }
 
 hipError_t launch_merge_split(const MergeArgs& a, int n_entries, hipStream_t s) {
     if (n_entries <= 0) return hipSuccess;

@@ -101,6 +101,15 @@ struct PrefixArgs {
     float scale_log2;
 };
 
+// The fused cascade step: n_dec balanced-decode workgroups (the suffix, plan in `d`) followed by
+// n_pre prefix workgroups (p.num_chunks items x Hkv kv heads, item table in p.items). The BalArgs
+// come first: the decode body reads them through the kernel argument pointer.
+struct StepArgs {
+    BalArgs    d;
+    PrefixArgs p;
+    int n_dec, n_pre;
+};
+
 // Kernel launchers (defined in the .hip files). Each returns the hipError_t of the launch.
 hipError_t launch_decode_partial(const PartialArgs& a, int G, hipStream_t s);
 hipError_t launch_merge_states(const float* part_o, const float* part_lse, _Float16* out,
@@ -109,6 +118,7 @@ hipError_t launch_decode_balanced(const BalArgs& a, int G, hipStream_t s);
 hipError_t launch_merge_split(const MergeArgs& a, int n_entries, hipStream_t s);
 hipError_t launch_fill_i32(int32_t* p, int32_t value, size_t n, hipStream_t s);
 hipError_t launch_cascade_prefix(const PrefixArgs& a, int G, int qtiles, hipStream_t s);
+hipError_t launch_cascade_step(const StepArgs& a, int G, hipStream_t s);
 hipError_t launch_append_kv(const AppendArgs& a, int cus, hipStream_t s);
 hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, int grid, hipStream_t s);
 hipError_t launch_flush(void* buf, size_t bytes, int grid, hipStream_t s);
@@ -117,6 +127,7 @@ hipError_t launch_flush(void* buf, size_t bytes, int grid, hipStream_t s);
 int occupancy_decode_partial(int G);
 int occupancy_decode_balanced(int G);
 int occupancy_cascade_prefix(int G);
+int occupancy_cascade_step(int G);   // workgroups of the fused step per CU
 int prefix_rows_per_workgroup();
 
 }  // namespace pdattn

@@ -41,7 +41,7 @@ EXPORTS = [
     "pdattn_plan_get_schedule", "pdattn_plan_upload", "pdattn_plan_run", "pdattn_plan_destroy",
     "pdattn_shared_prefix_pages", "pdattn_cascade_prefix",
     "pdattn_cascade_plan_create", "pdattn_cascade_tree_plan_create", "pdattn_cascade_plan_get_info",
-    "pdattn_cascade_decode", "pdattn_cascade_set_overlap",
+    "pdattn_cascade_decode", "pdattn_cascade_set_mode",
     "pdattn_cascade_plan_destroy",
     "pdattn_append_kv",
     "pdattn_stream_read", "pdattn_flush_cache", "pdattn_get_device_info",
@@ -97,7 +97,11 @@ class CascadeInfo(ctypes.Structure):
     _fields_ = [("use", ctypes.c_int), ("prefix_tokens", ctypes.c_int),
                 ("prefix_chunks", ctypes.c_int), ("prefix_workgroups", ctypes.c_int),
                 ("suffix_workgroups", ctypes.c_int), ("workspace_bytes", ctypes.c_size_t),
-                ("nodes", ctypes.c_int), ("levels", ctypes.c_int)]
+                ("nodes", ctypes.c_int), ("levels", ctypes.c_int), ("mode", ctypes.c_int)]
+
+
+# pdattn_cascade_set_mode
+CASCADE_FUSED, CASCADE_SERIAL, CASCADE_TWO_STREAMS = 0, 1, 2
 
 
 class DeviceInfo(ctypes.Structure):
@@ -152,7 +156,7 @@ def lib():
                                              ctypes.POINTER(P)], I),
         "pdattn_cascade_plan_get_info": ([P, ctypes.POINTER(CascadeInfo)], I),
         "pdattn_cascade_decode": ([P, P, P, ctypes.POINTER(Workspace), P], I),
-        "pdattn_cascade_set_overlap": ([P, I], I),
+        "pdattn_cascade_set_mode": ([P, I], I),
         "pdattn_cascade_plan_destroy": ([P], None),
         "pdattn_append_kv": ([P, P, P, P, P, P, P, P, I, I, I, P, P], I),
         "pdattn_stream_read": ([P, S, P, P], I),
@@ -372,10 +376,9 @@ class CascadePlan:
         _check(lib().pdattn_cascade_decode(self._h, ptr(out), ptr(lse), ctypes.byref(ws), stream_ptr(stream)),
                "pdattn_cascade_decode")
 
-    def set_overlap(self, enable: bool):
-        """Prefix launches on the plan's second stream, concurrent with the suffix decode (the
-        default), or every launch on the caller's stream (pdattn_cascade_set_overlap)."""
-        _check(lib().pdattn_cascade_set_overlap(self._h, int(bool(enable))), "pdattn_cascade_set_overlap")
+    def set_mode(self, mode: int):
+        """CASCADE_FUSED, CASCADE_SERIAL or CASCADE_TWO_STREAMS (pdattn_cascade_set_mode)."""
+        _check(lib().pdattn_cascade_set_mode(self._h, int(mode)), "pdattn_cascade_set_mode")
 
     def close(self):
         if self._h:

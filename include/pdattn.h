@@ -200,6 +200,19 @@ int pdattn_cascade_prefix(const pdattn_prefix_params* p, void* stream);
 
 typedef struct pdattn_cascade_plan pdattn_cascade_plan;
 
+/* How pdattn_cascade_decode runs the prefix pass and the suffix decode (pdattn_cascade_set_mode).
+ * FUSED: one launch whose first workgroups decode the suffix and whose others run the prefix
+ * items; both roles are 4-wave workgroups small enough for a CU to hold one of each, so every CU
+ * streams suffix pages while its matrix core works on the prefix. Default where two of these
+ * workgroups fit on a CU (G = 1, 2, 4). SERIAL: the prefix launch, then the suffix decode (the
+ * reference's order, cascade_decode 01_decode_attention.cu:703-712); default at G = 8. TWO_STREAMS:
+ * the prefix launch forked onto a second stream owned by the plan, joined before the merge. All
+ * three compute the same partials with the same kernels' arithmetic: the results are bitwise
+ * equal. The merge launch follows in every mode. */
+#define PDATTN_CASCADE_FUSED       0
+#define PDATTN_CASCADE_SERIAL      1
+#define PDATTN_CASCADE_TWO_STREAMS 2
+
 typedef struct pdattn_cascade_info {
     int    use;             /* 1 when a shared prefix of >= min_prefix tokens was found  */
     int    prefix_tokens;   /* Lp (of the first node)                                   */
@@ -209,6 +222,7 @@ typedef struct pdattn_cascade_info {
     size_t workspace_bytes;
     int    nodes;           /* shared-prefix nodes (1 for the reference's rule)        */
     int    levels;          /* depth of the node tree                                  */
+    int    mode;            /* PDATTN_CASCADE_*                                        */
 } pdattn_cascade_info;
 
 /* Build the cascade plan (plan_cascade, 01_decode_attention.cu:664-701) from the launch block
@@ -233,19 +247,17 @@ int pdattn_cascade_tree_plan_create(const pdattn_decode_params* base, const int3
                                     const int32_t* d_indices, int min_prefix,
                                     pdattn_cascade_plan** plan);
 int pdattn_cascade_plan_get_info(const pdattn_cascade_plan* plan, pdattn_cascade_info* info);
-/* Prefix kernel, suffix decode and merge on `stream` (cascade_decode, 01_decode_attention.cu:703-712).
- * The first call with a given workspace uploads the plan's schedule into it (stream-ordered). */
+/* Prefix pass, suffix decode and merge on `stream` (cascade_decode, 01_decode_attention.cu:703-712),
+ * as the plan's mode says. The first call with a given workspace uploads the plan's schedule into
+ * it (stream-ordered). */
 int pdattn_cascade_decode(pdattn_cascade_plan* plan, void* out, float* lse, pdattn_workspace* ws,
                           void* stream);
-/* Prefix/suffix overlap (off by default). With enable = 1, pdattn_cascade_decode forks the prefix
- * launches onto a second stream owned by the plan (created on first use, default priority) and
- * joins it back into `stream` before the merge, so the prefix MFMA pass and the suffix decode can
- * run concurrently; the step stays graph-capturable. The results are bitwise the same either way.
- * The reference lists this as not done (README.md:73). On MI355X the cross-queue fork and join
- * each add several microseconds and the two kernels cannot share a CU (registers), so the single
- * stream is faster at the benchmark's shapes; the option is for callers whose prefix pass is long
- * enough to hide them. */
-int pdattn_cascade_set_overlap(pdattn_cascade_plan* plan, int enable);
+/* Choose how the prefix pass and the suffix decode run (PDATTN_CASCADE_*): both overlap (FUSED,
+ * TWO_STREAMS) or not (SERIAL). The reference lists prefix/suffix overlap as not done
+ * (README.md:73). FUSED is rejected (PDATTN_ERR_UNSUPPORTED) where its workgroups do not fit two
+ * per CU. The TWO_STREAMS stream is created on first use with the default priority; the step
+ * stays graph-capturable in every mode. */
+int pdattn_cascade_set_mode(pdattn_cascade_plan* plan, int mode);
 void pdattn_cascade_plan_destroy(pdattn_cascade_plan* plan);
 
 /* ---- paged KV append ---------------------------------------------------------------------- */

@@ -163,9 +163,9 @@ def test_tree_cascade_without_sharing_falls_back():
 
 
 @pytest.mark.parametrize("tree", [False, True], ids=["single-level", "tree"])
-def test_overlap_on_and_off_bitwise_equal(tree):
-    """Prefix launches forked onto the plan's second stream or on the caller's stream (the
-    default): the same kernels, so the same bits; both against the oracle."""
+def test_cascade_modes_bitwise_equal(tree):
+    """The fused step (the default at G=4), separate launches on one stream, and the prefix
+    forked onto a second stream: the same arithmetic, so the same bits; against the oracle."""
     import torch
 
     import _gpu
@@ -182,10 +182,11 @@ def test_overlap_on_and_off_bitwise_equal(tree):
     ws = pdattn.Workspace()
     got = []
     try:
-        assert cp.info().use == 1
+        assert cp.info().use == 1 and cp.info().mode == pdattn.CASCADE_FUSED
         s = torch.cuda.current_stream()
-        for enable in (True, False, True):
-            cp.set_overlap(enable)
+        for mode in (pdattn.CASCADE_FUSED, pdattn.CASCADE_SERIAL, pdattn.CASCADE_TWO_STREAMS,
+                     pdattn.CASCADE_FUSED):
+            cp.set_mode(mode)
             db.out.fill_(float("nan"))
             db.lse.fill_(float("nan"))
             cp.decode(db.out, db.lse, ws, s)
@@ -199,6 +200,31 @@ def test_overlap_on_and_off_bitwise_equal(tree):
         assert torch.equal(l.view(torch.int32), got[0][1].view(torch.int32))
     o = got[0][0].float().cpu().numpy().astype(np.float64)
     l = got[0][1].cpu().numpy().astype(np.float64)
+    ro, rl = _ref(bt)
+    check_out(o, ro)
+    check_lse(l, rl)
+
+
+def test_fused_mode_needs_two_workgroups_per_cu():
+    """At G=8 the fused step's workgroups do not fit two per CU: the plan defaults to separate
+    launches and refuses the fused mode; an unknown mode is refused everywhere."""
+    import _gpu
+    import pdattn
+    bt = inputs.make_shared_prefix_batch(256, [5, 40, 17], 32, 4, seed=63)
+    db = _gpu.DeviceBatch(bt)
+    cp = pdattn.CascadePlan(db.params(), bt.indptr, bt.indices, bt.lens, db.indices, 16)
+    try:
+        assert cp.info().mode == pdattn.CASCADE_SERIAL
+        with pytest.raises(pdattn.PdattnError):
+            cp.set_mode(pdattn.CASCADE_FUSED)
+        with pytest.raises(pdattn.PdattnError):
+            cp.set_mode(7)
+        cp.set_mode(pdattn.CASCADE_TWO_STREAMS)
+        assert cp.info().mode == pdattn.CASCADE_TWO_STREAMS
+    finally:
+        cp.close()
+    o, l, info = _gpu.run_cascade(db, min_prefix=16)
+    assert info.use == 1
     ro, rl = _ref(bt)
     check_out(o, ro)
     check_lse(l, rl)

@@ -81,14 +81,15 @@ def test_cascade_graph():
 
 
 def test_cascade_two_streams_graph():
-    """The cascade with its prefix launches forked onto the plan's second stream: the fork / join
-    events are captured into the graph along with the launches."""
+    """The cascade with its prefix launch forked onto the plan's second stream: the fork / join
+    events are captured into the graph along with the launches. (test_cascade_graph covers the
+    default fused step.)"""
     bt = inputs.make_shared_prefix_batch(512, [40, 1, 300, 17, 64], 32, 8, seed=36)
     db = DeviceBatch(bt)
     print("graph: cascade, two streams", flush=True)
     cp = pdattn.CascadePlan(db.params(), bt.indptr, bt.indices, bt.lens, db.indices, 256)
     assert cp.info().use == 1
-    cp.set_overlap(True)
+    cp.set_mode(pdattn.CASCADE_TWO_STREAMS)
     ws = pdattn.Workspace()
     s = torch.cuda.current_stream()
     cp.decode(db.out, db.lse, ws, s)
