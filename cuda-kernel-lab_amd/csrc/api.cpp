@@ -575,16 +575,25 @@ int cascade_plan_create(const pdattn_decode_params* base, const int32_t* h_indpt
         // tokens ctok (a multiple of 64 in [256, 8192]) such that the sum over nodes of query
         // groups x Hkv x ceil(tokens / ctok) is about that target. Partial columns: one range per
         // depth, as wide as its node with the most chunks.
+        // Fused: a workgroup with few query rows is cheap (its waves hold one tile or none), so
+        // the target grows as the work-weighted rows per group fall below the 128 a workgroup
+        // holds: about one prefix workgroup per CU at 128 rows, up to three at 43 or fewer
+        // (measured best for 256-row single-level and 32-row tree nodes).
         cp->mode = f.occ_step[G] >= 2 ? PDATTN_CASCADE_FUSED : PDATTN_CASCADE_SERIAL;
-        const int target = cp->mode == PDATTN_CASCADE_FUSED ? f.cus : f.cus * std::max(1, f.occ_prefix[G]);
         int depths = 0;
         for (const CascadeNode& n : cp->nodes) depths = std::max(depths, n.depth + 1);
         std::vector<int> depth_cols(depths, 0);
-        double units = 0;
+        double units = 0, row_units = 0;
         for (CascadeNode& n : cp->nodes) {
+            const int Lp = (n.p1 - n.p0) * kPage;
             n.qgroups = (n.ns * G + prefix_rows_per_workgroup() - 1) / prefix_rows_per_workgroup();
-            units += (double)n.qgroups * base->Hkv * (n.p1 - n.p0) * kPage;
+            units += (double)n.qgroups * base->Hkv * Lp;
+            row_units += (double)n.ns * G * base->Hkv * Lp;
         }
+        const double grp_rows = units > 0 ? row_units / units : prefix_rows_per_workgroup();
+        const double scale = std::min(3.0, std::max(1.0, prefix_rows_per_workgroup() / grp_rows));
+        const int target = cp->mode == PDATTN_CASCADE_FUSED ? (int)(f.cus * scale)
+                                                             : f.cus * std::max(1, f.occ_prefix[G]);
         int ctok = (int)(units / target);
         ctok = std::min(std::max((ctok + 63) / 64 * 64, 256), 8192);
         for (CascadeNode& n : cp->nodes) {
