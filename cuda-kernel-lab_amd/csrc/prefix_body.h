@@ -190,8 +190,20 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
             }
         }
 
-        // online softmax (base 2) per query
+        // Online softmax (base 2) per query. The scores stay unscaled: the maximum is taken on
+        // them and scaled once (the scale is positive, so this is the maximum of the scaled
+        // scores), and each weight is exp2(fma(s, scale, -m)). Only a block that runs past the
+        // chunk's end masks its keys (to -inf, weight 0).
         const int kbase = kbeg + kb * KB + 4 * lg;
+        if (kbeg + (kb + 1) * KB > kend) {
+#pragma unroll
+            for (int tq = 0; tq < NT; ++tq)
+#pragma unroll
+                for (int tk = 0; tk < 4; ++tk)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (kbase + 16 * tk + j >= kend) s[tq][tk][j] = -INFINITY;
+        }
         float mn[NT];
         bool grow = false;
 #pragma unroll
@@ -200,15 +212,10 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
 #pragma unroll
             for (int tk = 0; tk < 4; ++tk)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const bool ok = kbase + 16 * tk + j < kend;
-                    const float x = ok ? s[tq][tk][j] * a.scale_log2 : -INFINITY;
-                    s[tq][tk][j] = x;
-                    mx = fmaxf(mx, x);
-                }
+                for (int j = 0; j < 4; ++j) mx = fmaxf(mx, s[tq][tk][j]);
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = fmaxf(mx, __shfl_xor(mx, 32));
-            mn[tq] = fmaxf(m_run[tq], mx);
+            mn[tq] = fmaxf(m_run[tq], mx * a.scale_log2);
             grow |= mn[tq] > m_run[tq];
         }
         if (__builtin_amdgcn_ballot_w64(grow)) {
@@ -229,7 +236,7 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
             for (int tk = 0; tk < 4; ++tk)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const float p = __builtin_amdgcn_exp2f(s[tq][tk][j] - ms);
+                    const float p = __builtin_amdgcn_exp2f(fmaf(s[tq][tk][j], a.scale_log2, -ms));
                     l_run[tq] += p;   // fp32 weights for the denominator (exact lse); PV uses
                     pb[tq][tk >> 1][(tk & 1) * 4 + j] = (_Float16)p;   // them rounded to nearest
                 }
