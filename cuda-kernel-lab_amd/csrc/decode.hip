@@ -841,9 +841,12 @@ int occupancy_of(const void* fn, int threads) {
 template <int G>
 using PartialCfg = Cfg<G, (G >= 8 ? 16 : 8), 8, 2>;
 // Balanced launch: 4 waves (one per SIMD, one workgroup per CU), 16 lanes per row (four row groups
-// per wave, so the end-of-segment merge is two permlane steps), a four-page ring.
+// per wave, so the end-of-segment merge is two permlane steps), a two-page ring: one page in
+// flight while the other is computed. Deeper rings measured slower at every shape (4 pages:
+// 30.6 vs 28.5 us back to back at 1x32K, 46.1 vs 44.9 us at 64x1K): more bytes in flight only
+// lengthen the memory queues. G = 8 keeps three pages.
 #ifndef PD_BAL_NBUF
-#define PD_BAL_NBUF 4
+#define PD_BAL_NBUF 2
 #endif
 template <int G>
 using BalCfg = Cfg<G, 16, 4, (G >= 8 ? 3 : PD_BAL_NBUF)>;
