@@ -6,28 +6,32 @@
 // as a normalized partial (o, lse), then a log-sum-exp merge of the partials.
 //
 // How it maps to CDNA4:
-//  * A workgroup is 8 waves; all of them work on one (sequence, kv head) token range, each wave
-//    on every 8th page of it. K and V rows go straight from HBM into VGPRs with 16-byte
-//    non-temporal loads: a 256-byte row (128 fp16) is read by LPR lanes, so one wave-wide load
-//    instruction reads 64/LPR rows of one page, each as whole 128-byte lines. No LDS staging is
-//    needed because every lane reads only the bytes it computes with.
+//  * Two workgroup shapes. The uniform split (decode_partial_kernel, the reference's launch
+//    shape) is 8 waves on one (sequence, kv head, chunk), each wave on every 8th page. The
+//    balanced decode (decode_balanced_kernel, the plan/run path) is 4 waves, one per SIMD and one
+//    workgroup per CU, walking a planned list of segments, each wave on every 4th page.
+//  * K and V rows go straight from HBM into VGPRs with 16-byte non-temporal loads: a 256-byte
+//    row (128 fp16) is read by LPR lanes, so one wave-wide load instruction reads 64/LPR rows of
+//    one page, each as whole 128-byte lines. No LDS staging is needed because every lane reads
+//    only the bytes it computes with.
 //  * Scores: each lane takes the fp16 dot product of its slice of q_h and k_j with
 //    v_dot2_f32_f16 (fp32 accumulate), then the LPR lanes of a row sum with DPP row ops
 //    (quad_perm, row_half_mirror, row_mirror), which leaves the score in every lane of the row.
 //  * Every lane therefore owns whole keys: it keeps its own online-softmax state (max, sum,
 //    output slice) over the keys it holds, so the PV product needs no cross-lane traffic. The
-//    64/LPR independent states of a wave are merged once at the end in the VALU (DPP row_ror and
-//    v_permlane16/32_swap), and the eight waves of the workgroup through LDS.
+//    64/LPR independent states of a wave are merged once at the end, in the VALU (DPP row_ror and
+//    v_permlane16/32_swap) or through LDS, and the waves of the workgroup through LDS.
 //  * Softmax runs in base 2 on log2(e)-prescaled scores with v_exp_f32 / v_log_f32
 //    (exp(x) = 2^(x log2 e)); the running output is rescaled only when some lane's max grows
 //    (a wave-uniform branch), which after the first pages is rare.
-//  * Prefetch: a two-page ring in VGPRs; the loads of the next page are issued before the
-//    current page is computed.
+//  * Prefetch: a two-page ring in VGPRs (three pages for the balanced decode at G = 8); the
+//    loads of the next page are issued before the current page is computed.
 //
 // Lane geometry, G = query heads per kv head:
-//   G <= 4: LPR = 8 lanes per row, 8 rows per load, each lane holds 2 rows x 16 dims of a page;
-//   G == 8: LPR = 16, 4 rows per load, each lane holds 4 rows x 8 dims (keeps the fp32 output
-//           state at 64 VGPRs).
+//   uniform split, G <= 4: LPR = 8 lanes per row, 8 rows per load, each lane holds 2 rows x 16
+//           dims of a page;
+//   uniform split at G == 8, and the balanced decode: LPR = 16, 4 rows per load, each lane holds
+//           4 rows x 8 dims (keeps the fp32 output state at 64 VGPRs at G = 8).
 // Lane (r = lane / LPR, c = lane % LPR) holds rows i*RPI + r of each page and the 16-byte pieces
 // kk*LPR + c (dims 8*(kk*LPR + c) .. +7), kk < PPL.
 #include <math.h>

@@ -177,7 +177,7 @@ def test_cascade_modes_bitwise_equal(tree):
     else:
         bt = inputs.make_shared_prefix_batch(1024, [1] * 70, 32, 8, seed=62)
     db = _gpu.DeviceBatch(bt)
-    print(f"cascade overlap on/off: tree={tree}", flush=True)
+    print(f"cascade modes: tree={tree}", flush=True)
     cp = pdattn.CascadePlan(db.params(), bt.indptr, bt.indices, bt.lens, db.indices, 16, tree)
     ws = pdattn.Workspace()
     got = []
