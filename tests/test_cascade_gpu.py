@@ -228,3 +228,25 @@ def test_fused_mode_needs_two_workgroups_per_cu():
     ro, rl = _ref(bt)
     check_out(o, ro)
     check_lse(l, rl)
+
+
+def test_many_short_sequences_grow_the_suffix_grid():
+    """3500 sequences of 1..16 private tokens behind a 64-token prefix: 7000 (sequence, kv head)
+    pairs need more than one suffix workgroup per CU (at most 24 segments each), so the fused
+    step's prefix blocks start after a grid larger than the CU count."""
+    import _gpu
+    import pdattn
+    rng = np.random.default_rng(64)
+    suffix = [int(x) for x in rng.integers(1, 17, size=3500)]
+    bt = inputs.make_shared_prefix_batch(64, suffix, 8, 2, seed=64)
+    db = _gpu.DeviceBatch(bt)
+    print("cascade: 3500 short sequences", flush=True)
+    cp = pdattn.CascadePlan(db.params(), bt.indptr, bt.indices, bt.lens, db.indices, 16)
+    info = cp.info()
+    cp.close()
+    assert info.use == 1 and info.mode == pdattn.CASCADE_FUSED
+    assert info.suffix_workgroups > pdattn.device_info().compute_units
+    o, l, info = _gpu.run_cascade(db, min_prefix=16)
+    ro, rl = _ref(bt)
+    check_out(o, ro)
+    check_lse(l, rl)
