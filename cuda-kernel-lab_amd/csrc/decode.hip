@@ -24,8 +24,8 @@
 //  * Softmax runs in base 2 on log2(e)-prescaled scores with v_exp_f32 / v_log_f32
 //    (exp(x) = 2^(x log2 e)); the running output is rescaled only when some lane's max grows
 //    (a wave-uniform branch), which after the first pages is rare.
-//  * Prefetch: a two-page ring in VGPRs (three pages for the balanced decode at G = 8); the
-//    loads of the next page are issued before the current page is computed.
+//  * Prefetch: a two-page ring in VGPRs; the loads of the next page are issued before the
+//    current page is computed.
 //
 // Lane geometry, G = query heads per kv head:
 //   uniform split, G <= 4: LPR = 8 lanes per row, 8 rows per load, each lane holds 2 rows x 16
@@ -847,13 +847,16 @@ using PartialCfg = Cfg<G, (G >= 8 ? 16 : 8), 8, 2>;
 // Balanced launch: 4 waves (one per SIMD, one workgroup per CU), 16 lanes per row (four row groups
 // per wave, so the end-of-segment merge is two permlane steps), a two-page ring: one page in
 // flight while the other is computed. Deeper rings measured slower at every shape (4 pages:
-// 30.6 vs 28.5 us back to back at 1x32K, 46.1 vs 44.9 us at 64x1K): more bytes in flight only
-// lengthen the memory queues. G = 8 keeps three pages.
+// 30.6 vs 28.5 us back to back at 1x32K, 46.1 vs 44.9 us at 64x1K; at G = 8, 3 pages: 29.3 vs
+// 28.6 us and 42.8 vs 41.4 us): more bytes in flight only lengthen the memory queues.
 #ifndef PD_BAL_NBUF
 #define PD_BAL_NBUF 2
 #endif
+#ifndef PD_BAL_NBUF8
+#define PD_BAL_NBUF8 2
+#endif
 template <int G>
-using BalCfg = Cfg<G, 16, 4, (G >= 8 ? 3 : PD_BAL_NBUF)>;
+using BalCfg = Cfg<G, 16, 4, (G >= 8 ? PD_BAL_NBUF8 : PD_BAL_NBUF)>;
 
 template <class C>
 void launch_p(const PartialArgs& a, hipStream_t s) {
