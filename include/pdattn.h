@@ -91,10 +91,10 @@ void pdattn_workspace_release(pdattn_workspace* ws);
 
 /* ---- reference-shaped split-KV path (uniform chunks) ------------------------------------- */
 
-/* Chunk count for the uniform split (plan_chunks, 01_decode_attention.cu:289-312): about one full
- * wave of resident workgroups over all CUs (hipOccupancyMaxActiveBlocksPerMultiprocessor x CU
- * count, rounded down), chunks of at least 256 tokens, chunk_tokens a multiple of 16;
- * force_chunks > 0 overrides. `variant` is accepted for signature parity and must be 0..3. */
+/* Chunk count for the uniform split (plan_chunks, 01_decode_attention.cu:289-312): about one
+ * workgroup per CU over all (sequence, kv head) pairs (CU count / (B*Hkv), rounded down; the
+ * reference uses SM count x occupancy), chunks of at least 256 tokens, chunk_tokens a multiple of
+ * 16; force_chunks > 0 overrides. `variant` is accepted for signature parity and must be 0..3. */
 int pdattn_plan_chunks(int G, int variant, int B, int Hkv, int max_len, int force_chunks,
                        int* num_chunks, int* chunk_tokens);
 
