@@ -144,6 +144,8 @@ PartialArgs to_partial_args(const pdattn_decode_params* p) {
     a.kv_last = p->kv_last_page_len;
     a.part_o = p->part_o;
     a.part_lse = p->part_lse;
+    a.out = nullptr;
+    a.lse = nullptr;
     a.B = p->B;
     a.Hq = p->Hq;
     a.Hkv = p->Hkv;
@@ -773,7 +775,16 @@ int pdattn_decode_attention(const pdattn_decode_params* p, int G, int variant, v
     pdattn_decode_params q = *p;
     if (int st = pdattn_workspace_partials(ws, p->B, p->Hq, p->part_stride, &q.part_o, &q.part_lse)) return st;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    PD_HIP(launch_decode_partial(to_partial_args(&q), G, s));
+    PartialArgs a = to_partial_args(&q);
+    if (p->num_chunks == 1) {
+        // one chunk per sequence: the partial kernel writes the result (merge_states of a single
+        // state returns it unchanged), and the merge launch is skipped
+        a.out = static_cast<_Float16*>(out);
+        a.lse = lse;
+        PD_HIP(launch_decode_partial(a, G, s));
+        return PDATTN_OK;
+    }
+    PD_HIP(launch_decode_partial(a, G, s));
     PD_HIP(launch_merge_states(q.part_o, q.part_lse, static_cast<_Float16*>(out), lse, p->B * p->Hq,
                                p->part_stride, s));
     return PDATTN_OK;

@@ -458,6 +458,16 @@ __global__ __launch_bounds__(C::NT) void decode_partial_kernel(PartialArgs a) {
     const int kend = min(len, kbeg + a.chunk_tokens);
     process_range<C>(sm, a.q + ((size_t)b * a.Hq + kvh * G) * kHeadDim, a.k, a.v,
                      a.kv_indices + pb, 0, kbeg, kend, a.Hkv, kvh, a.scale_log2);
+    if (a.out != nullptr) {
+        // the only chunk: its normalized state is the result (the merge's weight would be 1)
+        const size_t row0 = (size_t)b * a.Hq + kvh * G;
+        for (int idx = threadIdx.x; idx < G * kHeadDim; idx += C::NT) {
+            const int h = idx / kHeadDim, d = idx % kHeadDim;
+            a.out[(row0 + h) * kHeadDim + d] = (_Float16)sm.fo[h][d];
+            if (d == 0) a.lse[row0 + h] = sm.flse[h];
+        }
+        return;
+    }
     for (int idx = threadIdx.x; idx < G * kHeadDim; idx += C::NT) {
         const int h = idx / kHeadDim, d = idx % kHeadDim;
         const size_t slot = ((size_t)b * a.Hq + kvh * G + h) * a.part_stride + a.chunk_base + chunk;

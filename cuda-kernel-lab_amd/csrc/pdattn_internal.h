@@ -21,6 +21,10 @@ struct PartialArgs {
     const int32_t*  kv_last;
     float*          part_o;
     float*          part_lse;
+    // Non-null (one chunk per sequence, nothing else to merge): the final fp16 out and lse are
+    // written here instead of the partial slots; a merge of one partial state would copy it.
+    _Float16*       out;
+    float*          lse;
     int B, Hq, Hkv, num_chunks, chunk_tokens, kv_start, chunk_base, part_stride;
     float scale_log2;         // sm_scale * log2(e)
 };

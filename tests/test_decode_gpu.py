@@ -89,6 +89,38 @@ def test_uniform_kv_start_matches_oracle():
         check_lse(l, rl, tag=f"kv_start={kv_start}")
 
 
+@pytest.mark.parametrize("kv_start", [0, 40])
+def test_single_chunk_skips_the_merge_bitwise(kv_start):
+    """decode_attention with one chunk per sequence writes out / lse from the partial kernel:
+    bitwise what decode_partial + merge_states give (a merge of one state returns it), and the
+    oracle's result; an empty sequence still gets 0 / -inf."""
+    import torch
+    import _gpu
+    import pdattn
+    bt = inputs.make_batch([0, 1, 300, 1000], 32, 8, seed=19)
+    db = _gpu.DeviceBatch(bt)
+    ct = 1024 - kv_start
+    p = db.params(1, ct, kv_start=kv_start)
+    ws = pdattn.Workspace()
+    pdattn.decode_attention(p, bt.G, db.out, db.lse, ws)
+    o1, l1 = db.results()
+    pdattn.workspace_release(ws)
+    rows = bt.B * bt.Hq
+    po, pl = _gpu.run_partials(db, 1, ct, kv_start)
+    out = torch.empty(rows, 128, dtype=torch.float16, device=_gpu.device())
+    lse = torch.empty(rows, dtype=torch.float32, device=_gpu.device())
+    pdattn.merge_states(torch.from_numpy(po.astype(np.float32)).to(out.device),
+                        torch.from_numpy(pl.astype(np.float32)).to(out.device), out, lse, rows, 1)
+    torch.cuda.synchronize()
+    o2 = out.float().cpu().numpy().astype(np.float64).reshape(o1.shape)
+    l2 = lse.cpu().numpy().astype(np.float64).reshape(l1.shape)
+    assert np.array_equal(o1, o2) and np.array_equal(l1, l2)
+    assert np.all(o1[0] == 0) and np.all(np.isneginf(l1[0]))
+    ro, rl = _ref(bt, kv_start)
+    check_out(o1, ro, tag=f"one chunk, kv_start={kv_start}")
+    check_lse(l1, rl, tag=f"one chunk, kv_start={kv_start}")
+
+
 def test_merge_states_matches_oracle():
     import torch
     import pdattn
