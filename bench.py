@@ -315,8 +315,8 @@ def cascade_workload(timer, args):
 
 def prefix_workload(timer, args):
     """The cascade's MFMA prefix pass alone (pdattn_cascade_prefix) on the benchmark's shared
-    prefix: 64 requests x 8192 shared tokens, chunks of 256 tokens (the plan's choice at this
-    shape, 256 workgroups). Flops per launch: 4 x (B Hq rows) x 128 x 8192 (QK^T and PV, 2 each)."""
+    prefix: 64 requests x 8192 shared tokens, chunks of 256 tokens (32 chunks x 2 query groups
+    of 128 rows x 8 kv heads = 512 workgroups). Flops per launch: 4 x (B Hq rows) x 128 x 8192 (QK^T and PV, 2 each)."""
     import numpy as np
     import torch
     import pdattn
@@ -349,7 +349,8 @@ def prefix_workload(timer, args):
     hot = e0.elapsed_time(e1) * 1e-3 / n
     flops = 4.0 * rows * 128 * Lp
     del t, po, pl
-    return {"flops": flops, "workgroups": nch * 8, "cold_us": round(cold * 1e6, 2),
+    qgroups = -(-(bt.B * 32 // 8) // 128)   # 128 stacked query rows per workgroup, per kv head
+    return {"flops": flops, "workgroups": nch * qgroups * 8, "cold_us": round(cold * 1e6, 2),
             "cold_TFLOP/s": round(flops / cold / 1e12, 1),
             "back_to_back_us": round(hot * 1e6, 2), "TFLOP/s": round(flops / hot / 1e12, 1),
             "frac_of_fp16_mfma_peak": round(flops / hot / 2.5e15, 4), "peak_TFLOP/s": 2500.0}

@@ -93,7 +93,8 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
     // Staging: thread t moves 16-byte chunk sc = t & 15 of K rows sr + SR i and of the V key
     // pairs (2 p, 2 p + 1), p = sr + SR i, sr = t >> 4. Keys past the chunk read the last valid
     // key instead (a real, finite row): their scores are masked to -inf below, so their weights
-    // are exactly 0.
+    // are exactly 0. The loads are cached: the other query groups of the chunk, placed on the
+    // same XCD, read the same lines.
     const int sc = tid & 15, sr = tid >> 4;
     pu32x4 kst[KPT], vst[2 * VPT];
     auto gload = [&](int kb) {
@@ -102,15 +103,15 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
         for (int i = 0; i < KPT; ++i) {
             const int key = min(key0 + sr + SR * i, kend - 1);
             const uint32_t pid = (uint32_t)sm.pg[(key - kbeg) >> 4];
-            kst[i] = __builtin_nontemporal_load(reinterpret_cast<const pu32x4*>(
-                a.k + pid * page_bytes + (size_t)(((key & 15) * a.Hkv + kvh) * 256 + sc * 16)));
+            kst[i] = *reinterpret_cast<const pu32x4*>(
+                a.k + pid * page_bytes + (size_t)(((key & 15) * a.Hkv + kvh) * 256 + sc * 16));
         }
 #pragma unroll
         for (int i = 0; i < 2 * VPT; ++i) {
             const int key = min(key0 + 2 * (sr + SR * (i >> 1)) + (i & 1), kend - 1);
             const uint32_t pid = (uint32_t)sm.pg[(key - kbeg) >> 4];
-            vst[i] = __builtin_nontemporal_load(reinterpret_cast<const pu32x4*>(
-                a.v + pid * page_bytes + (size_t)(((key & 15) * a.Hkv + kvh) * 256 + sc * 16)));
+            vst[i] = *reinterpret_cast<const pu32x4*>(
+                a.v + pid * page_bytes + (size_t)(((key & 15) * a.Hkv + kvh) * 256 + sc * 16));
         }
     };
     auto lstore = [&](int buf) {
