@@ -316,7 +316,8 @@ def cascade_workload(timer, args):
 def prefix_workload(timer, args):
     """The cascade's MFMA prefix pass alone (pdattn_cascade_prefix) on the benchmark's shared
     prefix: 64 requests x 8192 shared tokens, chunks of 256 tokens (32 chunks x 2 query groups
-    of 128 rows x 8 kv heads = 512 workgroups). Flops per launch: 4 x (B Hq rows) x 128 x 8192 (QK^T and PV, 2 each)."""
+    of 128 rows x 8 kv heads = 512 workgroups). Flops per launch: 4 x (B Hq rows) x 128 x 8192
+    (QK^T and PV, 2 each)."""
     import numpy as np
     import torch
     import pdattn
