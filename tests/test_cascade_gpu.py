@@ -93,6 +93,45 @@ def test_prefix_kernel_partials(chunk_tokens):
     assert lens
 
 
+@pytest.mark.parametrize("B,chunk_tokens", [(1, 64), (2, 96), (4, 128), (5, 96), (8, 256)])
+def test_small_groups_are_deterministic(B, chunk_tokens):
+    """Query groups of 4 to 32 rows (B x 4 heads here), which leave query tiles of the
+    workgroup empty: repeated launches give the same bits, and the partials match the oracle."""
+    import torch
+    import _gpu
+    import pdattn
+    Lp = 640
+    print(f"small prefix group: B={B} chunk_tokens={chunk_tokens}", flush=True)
+    bt = inputs.make_shared_prefix_batch(Lp, [16] * B, 32, 8, seed=8)
+    db = _gpu.DeviceBatch(bt)
+    nchunks = (Lp + chunk_tokens - 1) // chunk_tokens
+    rows = bt.B * bt.Hq
+    d = torch.device("cuda:0")
+    po = torch.full((rows, nchunks, 128), float("nan"), dtype=torch.float32, device=d)
+    pl = torch.full((rows, nchunks), float("nan"), dtype=torch.float32, device=d)
+    pp = pdattn.PrefixParams()
+    pp.q, pp.k_cache, pp.v_cache = db.q.data_ptr(), db.k.data_ptr(), db.v.data_ptr()
+    pp.prefix_pages = db.indices.data_ptr()
+    pp.part_o, pp.part_lse = po.data_ptr(), pl.data_ptr()
+    pp.B, pp.Hq, pp.Hkv = bt.B, bt.Hq, bt.Hkv
+    pp.prefix_len, pp.chunk_tokens, pp.part_stride = Lp, chunk_tokens, nchunks
+    pp.sm_scale = 1.0 / np.sqrt(128)
+    runs = []
+    for _ in range(6):
+        pdattn.cascade_prefix(pp)
+        torch.cuda.synchronize()
+        runs.append((po.clone(), pl.clone()))
+    for o, l in runs[1:]:
+        assert torch.equal(o.view(torch.int32), runs[0][0].view(torch.int32))
+        assert torch.equal(l.view(torch.int32), runs[0][1].view(torch.int32))
+    indptr = np.arange(bt.B + 1, dtype=np.int32) * (Lp // 16)
+    indices = np.concatenate([bt.indices[bt.indptr[b]:bt.indptr[b] + Lp // 16] for b in range(bt.B)])
+    last = np.full(bt.B, 16, np.int32)
+    ro, rl = oracle.partials(bt.q, bt.k, bt.v, indptr, indices, last, bt.Hq, bt.Hkv, nchunks, chunk_tokens)
+    check_lse(runs[0][1].cpu().numpy(), rl, tag="small group part_lse")
+    check_out(runs[0][0].cpu().numpy(), ro, tag="small group part_o")
+
+
 def test_unshared_batch_falls_back():
     """No shared pages: the plan reports use = 0 and the result equals plain decode
     (01_decode_attention.cu:810-815)."""
