@@ -200,6 +200,29 @@ def test_streamk_bitwise_deterministic():
             assert np.array_equal(o, first[0]) and np.array_equal(l, first[1])
 
 
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 8), (32, 8), (32, 4)], ids=["G1", "G2", "G4", "G8"])
+@pytest.mark.parametrize("path", ["streamk", "uniform"])
+def test_bitwise_deterministic_every_group_size(Hq, Hkv, path):
+    """Each kernel instantiation (G = 1, 2, 4, 8; balanced and uniform-split paths) gives the
+    same bits on repeated launches, with split pairs merged."""
+    import _gpu
+    print(f"determinism: {path} Hq={Hq} Hkv={Hkv}", flush=True)
+    bt = inputs.make_batch([3000, 777, 16, 1], Hq, Hkv, seed=12)
+    db = _gpu.DeviceBatch(bt)
+    first = None
+    for _ in range(4):
+        if path == "streamk":
+            o, l, info = _gpu.run_streamk(db, 61)
+            assert info.split_pairs > 0
+        else:
+            o, l, nc = _gpu.run_uniform(db, 5)
+            assert nc > 1
+        if first is None:
+            first = (o.copy(), l.copy())
+        else:
+            assert np.array_equal(o, first[0]) and np.array_equal(l, first[1])
+
+
 def test_page_permutation_invariance():
     """Moving the pages to other physical slots (and the page table with them) changes nothing."""
     import _gpu
