@@ -223,6 +223,33 @@ def test_bitwise_deterministic_every_group_size(Hq, Hkv, path):
             assert np.array_equal(o, first[0]) and np.array_equal(l, first[1])
 
 
+@pytest.mark.parametrize("seed", range(12))
+def test_random_batches_match_oracle(seed):
+    """Seeded random shapes: batch size, lengths (empty sequences and partial last pages
+    included), group size, forced grid and chunk size of the balanced planner, and forced chunk
+    counts of the uniform split."""
+    import _gpu
+    rng = np.random.default_rng(1000 + seed)
+    Hkv = int(rng.choice([1, 2, 4, 8]))
+    G = int(rng.choice([1, 2, 4, 8]))
+    B = int(rng.integers(1, 24))
+    lens = [int(x) for x in rng.integers(0, 2500, B)]
+    if rng.random() < 0.3:
+        lens[int(rng.integers(0, B))] = 0
+    wg = int(rng.choice([0, 1, 5, 33, 256, 700]))
+    print(f"random batch seed={seed}: B={B} Hq={G * Hkv} Hkv={Hkv} W={wg} lens={lens}", flush=True)
+    bt = inputs.make_batch(lens, G * Hkv, Hkv, seed=seed)
+    db = _gpu.DeviceBatch(bt)
+    ro, rl = _ref(bt)
+    o, l, info = _gpu.run_streamk(db, wg)
+    check_out(o, ro, tag=f"random stream-K seed={seed} W={info.workgroups}")
+    check_lse(l, rl, tag=f"random stream-K seed={seed}")
+    force = int(rng.integers(0, 9))
+    o, l, nc = _gpu.run_uniform(db, force)
+    check_out(o, ro, tag=f"random uniform seed={seed} chunks={nc}")
+    check_lse(l, rl, tag=f"random uniform seed={seed}")
+
+
 def test_page_permutation_invariance():
     """Moving the pages to other physical slots (and the page table with them) changes nothing."""
     import _gpu
