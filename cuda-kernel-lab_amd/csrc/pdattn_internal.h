@@ -84,6 +84,7 @@ struct AppendArgs {
     const int32_t*  positions;
     int32_t*        n_invalid;    // optional: tokens outside their sequence's pages
     int n, B, Hkv;
+    int tpb;                      // tokens per workgroup (set by launch_append_kv)
 };
 
 // Arguments of the MFMA shared-prefix kernel.

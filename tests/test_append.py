@@ -143,6 +143,23 @@ def test_append_prefill_style_and_invalid():
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("Hkv,lens", [(8, [2000, 1500, 37, 700]), (1, [20000, 15000, 3])])
+def test_append_prefill_many_tokens_per_workgroup(Hkv, lens):
+    """A prefill-sized append (thousands of tokens, so a workgroup takes 16 tokens at Hkv = 8 and
+    up to 128 at Hkv = 1): every position of every sequence, shuffled so that one workgroup's
+    tokens land in different pages and sequences, with invalid tokens at random places and a
+    token count that leaves a ragged last workgroup."""
+    rng = np.random.default_rng(5 + Hkv)
+    bidx = np.concatenate([np.full(L, b) for b, L in enumerate(lens)])
+    pos = np.concatenate([np.arange(L) for L in lens])
+    bad_b = rng.choice([-1, len(lens), 0], size=41)   # no such sequence, or sequence 0 ...
+    bad_p = np.where(bad_b == 0, -(-lens[0] // 16) * 16, 0)   # ... at the first position past its pages
+    bidx, pos = np.concatenate([bidx, bad_b]), np.concatenate([pos, bad_p])
+    perm = rng.permutation(len(bidx))
+    _gpu_append_case(lens, 4 * Hkv, Hkv, bidx[perm], pos[perm], seed=21)
+
+
+@pytest.mark.gpu
 def test_decode_after_append_matches_oracle():
     from _checks import check_lse, check_out
     from _gpu import run_streamk
