@@ -155,6 +155,33 @@ def ceiling_gbs(timer, steps):
     return nbytes / (statistics.median(ms) * 1e-3) / 1e9
 
 
+def size_matched_read_us(nbytes, stream, steps):
+    """Average duration of one stream_read launch over exactly `nbytes` (the workload's algorithmic
+    bytes, contiguous), timed like rotated_kernel_us: K launches back to back between one event
+    pair, launch i over buffer i mod n, the n buffers totalling >= ROT_BYTES. A single launch that
+    moves this many bytes pays the same launch, ramp-up and drain as the decode does, so this is the
+    achievable rate for a read of this size, beside the asymptotic 2 GiB ceiling."""
+    import torch
+    import pdattn
+    nbytes = (nbytes + 15) // 16 * 16
+    n = max(2, -(-ROT_BYTES // nbytes))
+    bufs = [torch.ones(nbytes // 4, dtype=torch.int32, device="cuda:0") for _ in range(n)]
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda:0")
+    for i in range(n):
+        pdattn.stream_read(bufs[i], nbytes, sink, stream)
+    k = max(steps, 4 * n)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(k):
+        pdattn.stream_read(bufs[i % n], nbytes, sink, stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    del bufs
+    return e0.elapsed_time(e1) * 1e3 / k
+
+
 def rotated_kernel_us(plan, ws, t, stream, steps):
     """Average duration of one balanced launch, K launches back to back between one event pair.
 
@@ -553,13 +580,22 @@ def main():
         result["stream_read_ceiling_GBs"] = round(ceil, 1)
         result["pct_of_ceiling"] = round(100 * value / ceil, 1)
         result["roofline"]["frac_of_ceiling"] = round(achieved / ceil, 4)
+        sm_us = size_matched_read_us(h["bytes"], timer.stream, args.steps)
+        result["roofline"]["size_matched_read"] = {
+            "bytes": h["bytes"], "us": round(sm_us, 2), "GB/s": round(gbs(h["bytes"], sm_us * 1e-6), 1),
+            "kernel_frac": round(sm_us / h["kernel_us"], 4),
+            "what": "stream_read over the workload's algorithmic bytes in one launch, back to back "
+                    "over rotated buffers (>= 1 GiB); kernel_frac = its time / the decode step's"}
         h2 = decode_workload(timer, [1024] * 64, args, with_uniform=False)
         v2, a2 = gbs(h2["bytes"], h2["ms"] * 1e-3), gbs(h2["bytes"], h2["kernel_us"] * 1e-6)
+        sm2_us = size_matched_read_us(h2["bytes"], timer.stream, args.steps)
         sec["64x1K"] = {"us_per_step": round(h2["ms"] * 1e3, 2), "GB/s": round(v2, 1),
                         "pct_of_peak": round(100 * v2 / PEAK_GBS, 1),
                         "pct_of_ceiling": round(100 * v2 / ceil, 1),
                         "kernel_us": round(h2["kernel_us"], 2), "kernel_GB/s": round(a2, 1),
                         "kernel_frac_of_ceiling": round(a2 / ceil, 4),
+                        "size_matched_read_us": round(sm2_us, 2),
+                        "kernel_frac_of_size_matched_read": round(sm2_us / h2["kernel_us"], 4),
                         "workgroups": h2["workgroups"], "algorithmic_bytes": h2["bytes"]}
         sec["cascade_64x(8192+512)"] = cascade_workload(timer, args)
         sec["cascade_prefix_mfma"] = prefix_workload(timer, args)

@@ -63,6 +63,28 @@ __device__ __forceinline__ pf32x4 mfma16x16x32(const pf16x8& a, const pf16x8& b,
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Max / sum over the four lanes l, l^16, l^32, l^48 (one column of a 16x16 accumulator), left in
+// all four, in the VALU: v_permlane16_swap pairs the 16-lane rows r and r^1, v_permlane32_swap the
+// rows r and r^2. After a swap of a value with its own copy, result 0 holds (in every lane) the
+// lower row's value and result 1 the upper row's, so the sum is formed in the same order in all
+// lanes. The copy goes through an empty asm statement: given one SSA value twice, the compiler
+// would treat the two results as equal and drop one.
+__device__ __forceinline__ unsigned pb_opaque(unsigned v) {
+    asm("" : "+v"(v));
+    return v;
+}
+template <bool MAX>
+__device__ __forceinline__ float col4_reduce(float v) {
+    unsigned x = __builtin_bit_cast(unsigned, v);
+    const auto r16 = __builtin_amdgcn_permlane16_swap(x, pb_opaque(x), false, false);
+    const float a = __builtin_bit_cast(float, (unsigned)r16[0]), b = __builtin_bit_cast(float, (unsigned)r16[1]);
+    v = MAX ? fmaxf(a, b) : a + b;
+    x = __builtin_bit_cast(unsigned, v);
+    const auto r32 = __builtin_amdgcn_permlane32_swap(x, pb_opaque(x), false, false);
+    const float c = __builtin_bit_cast(float, (unsigned)r32[0]), d = __builtin_bit_cast(float, (unsigned)r32[1]);
+    return MAX ? fmaxf(c, d) : c + d;
+}
+
 // The work of one workgroup with NT query tiles per wave. Query tile tq of a wave is tile
 // tq * PW + wave of the group's rows, so a group of up to 16 * PW * NT rows occupies the first
 // NT tiles of every wave.
@@ -214,8 +236,7 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
             for (int tk = 0; tk < 4; ++tk)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) mx = fmaxf(mx, s[tq][tk][j]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            mx = col4_reduce<true>(mx);
             mn[tq] = fmaxf(m_run[tq], mx * a.scale_log2);
             grow |= mn[tq] > m_run[tq];
         }
@@ -268,9 +289,7 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
     // normalized partial of this chunk
 #pragma unroll
     for (int tq = 0; tq < NT; ++tq) {
-        float L = l_run[tq];
-        L += __shfl_xor(L, 16);
-        L += __shfl_xor(L, 32);
+        const float L = col4_reduce<false>(l_run[tq]);
         if (qrow[tq] < 0) continue;
         const size_t slot = (size_t)qrow[tq] * a.part_stride + a.col0 + chunk;
         const float inv = L > 0.f ? 1.f / L : 0.f;
