@@ -550,7 +550,7 @@ def main():
     lens = [1024] * 64 if args.only == "64x1k" else [32768]
     name = ("paged GQA decode B=64 L=1024 (metric's 64x1K)" if args.only == "64x1k"
             else "paged GQA decode B=1 L=32768 (configs[1])")
-    h = decode_workload(timer, lens, args, with_uniform=not args.only)
+    h = decode_workload(timer, lens, args, with_uniform=args.only in ("", "32k", "64x1k"))
     value = gbs(h["bytes"], h["ms"] * 1e-3)
     achieved = gbs(h["bytes"], h["kernel_us"] * 1e-6)
     traffic = measured_traffic() if not args.only or args.only == "32k" else None
@@ -586,7 +586,7 @@ def main():
             "kernel_frac": round(sm_us / h["kernel_us"], 4),
             "what": "stream_read over the workload's algorithmic bytes in one launch, back to back "
                     "over rotated buffers (>= 1 GiB); kernel_frac = its time / the decode step's"}
-        h2 = decode_workload(timer, [1024] * 64, args, with_uniform=False)
+        h2 = decode_workload(timer, [1024] * 64, args, with_uniform=True)
         v2, a2 = gbs(h2["bytes"], h2["ms"] * 1e-3), gbs(h2["bytes"], h2["kernel_us"] * 1e-6)
         sm2_us = size_matched_read_us(h2["bytes"], timer.stream, args.steps)
         sec["64x1K"] = {"us_per_step": round(h2["ms"] * 1e3, 2), "GB/s": round(v2, 1),
@@ -596,7 +596,8 @@ def main():
                         "kernel_frac_of_ceiling": round(a2 / ceil, 4),
                         "size_matched_read_us": round(sm2_us, 2),
                         "kernel_frac_of_size_matched_read": round(sm2_us / h2["kernel_us"], 4),
-                        "workgroups": h2["workgroups"], "algorithmic_bytes": h2["bytes"]}
+                        "workgroups": h2["workgroups"], "algorithmic_bytes": h2["bytes"],
+                        "uniform_path": h2["uniform"]}
         sec["cascade_64x(8192+512)"] = cascade_workload(timer, args)
         sec["cascade_prefix_mfma"] = prefix_workload(timer, args)
         sec["append_kv"] = append_workload(timer, args)

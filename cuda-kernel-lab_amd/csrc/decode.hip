@@ -155,19 +155,25 @@ struct Smem {
     float flse[G];            // combined lse (natural log)
 };
 
+// A page of one kv head seen through a buffer resource: base = cache + page * page_bytes +
+// kvh * 256, num_records = the bytes from there to the end of the page, so every lane's offset is
+// in range. A padding slot of the ring uses num_records = 0: its loads return zeros without a
+// memory access, while the ring still issues the same loads in every slot (exact wait counts).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const uint8_t* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
 template <class C>
-__device__ __forceinline__ void load_page(PageRegs<C>& pr, const uint8_t* kp, const uint8_t* vp,
-                                          uint32_t lbase, uint32_t rstride) {
-    using g = C;
+__device__ __forceinline__ void load_page_rsrc(PageRegs<C>& pr, __amdgpu_buffer_rsrc_t rk,
+                                               __amdgpu_buffer_rsrc_t rv, uint32_t lbase, uint32_t rstride) {
 #pragma unroll
-    for (int i = 0; i < g::RG; ++i)
+    for (int i = 0; i < C::RG; ++i)
 #pragma unroll
-        for (int kk = 0; kk < g::PPL; ++kk) {
-            const uint32_t off = lbase + i * rstride + kk * (g::LPR * 16);
-            // K/V bytes are read exactly once: non-temporal loads keep them from displacing
-            // reusable lines in L2 and the Infinity Cache
-            pr.k[i][kk] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kp + off));
-            pr.v[i][kk] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vp + off));
+        for (int kk = 0; kk < C::PPL; ++kk) {
+            const int off = (int)(lbase + i * rstride + kk * (C::LPR * 16));
+            // aux = 2: non-temporal (K/V bytes are read once)
+            pr.k[i][kk] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 2);
+            pr.v[i][kk] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 2);
         }
 }
 
@@ -248,7 +254,9 @@ __device__ __forceinline__ void process_range(Smem<C::G, C::NW>& sm, const _Floa
                               int Hkv, int kvh, float scale2) {
     using g = C;
     constexpr int G = C::G, NW = C::NW, NBUF = C::NBUF;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the wave index is made wave-uniform explicitly: the page counts and buffer resources derived
+    // from it must live in scalar registers (a non-uniform resource turns each load into a loop)
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int r = lane / g::LPR, c = lane % g::LPR;
 
     f16x2 qv[G][g::PPL][4];
@@ -275,32 +283,40 @@ __device__ __forceinline__ void process_range(Smem<C::G, C::NW>& sm, const _Floa
         const int pfirst = (t0 - tok_base) / kPage, plast = (t1 - 1 - tok_base) / kPage;
         const int npg = plast - pfirst + 1;
         const int nmine = npg > wave ? (npg - wave + NW - 1) / NW : 0;
-        const size_t page_bytes = (size_t)kPage * Hkv * 256;
-        const uint32_t lbase = (uint32_t)((r * Hkv + kvh) * 256 + c * 16);
+        const uint32_t page_bytes = (uint32_t)(kPage * Hkv * 256);
+        const uint32_t lbase = (uint32_t)(r * Hkv * 256 + c * 16);
         const uint32_t rstride = (uint32_t)(g::RPI * Hkv * 256);
+        // slot j of the window: page j of it through a buffer resource over the rest of the page
+        // (from this kv head's row), or, past the end, a zero-length resource whose loads return
+        // zeros without a memory access, so every iteration issues the same loads (exact waits)
+        // and no page is read twice
+        auto issue = [&](PageRegs<C>& b, int pidv, int j, int cnt) {
+            const uint8_t* kb = kbase;
+            const uint8_t* vb = vbase;
+            uint32_t nrec = 0;
+            if (j < cnt) {
+                const size_t off = (size_t)(uint32_t)__builtin_amdgcn_readlane(pidv, j) * page_bytes +
+                                   (size_t)kvh * 256;
+                kb += off;
+                vb += off;
+                nrec = page_bytes - (uint32_t)kvh * 256;
+            }
+            load_page_rsrc<C>(b, page_rsrc(kb, nrec), page_rsrc(vb, nrec), lbase, rstride);
+        };
         for (int base = 0; base < nmine; base += 64) {
             const int cnt = min(64, nmine - base);
             // lane j holds the physical page of this wave's (base + j)-th page
             const int pidv = lane < cnt ? pages[pfirst + wave + NW * (base + lane)] : 0;
             // ring of NBUF pages in VGPRs: page i lives in buf[i % NBUF]; NBUF-1 are in flight
-            // while one is computed. Past the end the last page is loaded again (an L2 hit), so
-            // every iteration issues the same loads and the wait counts stay exact.
+            // while one is computed
             PageRegs<C> buf[NBUF];
 #pragma unroll
-            for (int u = 0; u < NBUF - 1; ++u) {
-                const size_t pid = (uint32_t)__builtin_amdgcn_readlane(pidv, min(u, cnt - 1));
-                load_page<C>(buf[u], kbase + pid * page_bytes, vbase + pid * page_bytes, lbase, rstride);
-            }
+            for (int u = 0; u < NBUF - 1; ++u) issue(buf[u], pidv, u, cnt);
             for (int it = 0; it < cnt; it += NBUF) {
 #pragma unroll
                 for (int u = 0; u < NBUF; ++u) {
                     if (it + u >= cnt) break;
-                    {
-                        const int nx = min(it + u + NBUF - 1, cnt - 1);
-                        const size_t pid = (uint32_t)__builtin_amdgcn_readlane(pidv, nx);
-                        load_page<C>(buf[(u + NBUF - 1) % NBUF], kbase + pid * page_bytes,
-                                     vbase + pid * page_bytes, lbase, rstride);
-                    }
+                    issue(buf[(u + NBUF - 1) % NBUF], pidv, it + u + NBUF - 1, cnt);
                     page_step<C>(st, buf[u], qv, tok_base + (pfirst + wave + NW * (base + it + u)) * kPage + r,
                                  t0, t1, scale2);
                 }
@@ -517,28 +533,6 @@ __global__ __launch_bounds__(kMergeThreads) void merge_split_kernel(MergeArgs a)
                   }
               },
               red, a.out + row * kHeadDim, a.lse + row);
-}
-
-// A page of one kv head seen through a buffer resource: base = cache + page * page_bytes +
-// kvh * 256, num_records = the bytes from there to the end of the page, so every lane's offset is
-// in range. A padding slot of the ring uses num_records = 0: its loads return zeros without a
-// memory access, while the ring still issues the same loads in every slot (exact wait counts).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const uint8_t* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-template <class C>
-__device__ __forceinline__ void load_page_rsrc(PageRegs<C>& pr, __amdgpu_buffer_rsrc_t rk,
-                                               __amdgpu_buffer_rsrc_t rv, uint32_t lbase, uint32_t rstride) {
-#pragma unroll
-    for (int i = 0; i < C::RG; ++i)
-#pragma unroll
-        for (int kk = 0; kk < C::PPL; ++kk) {
-            const int off = (int)(lbase + i * rstride + kk * (C::LPR * 16));
-            // aux = 2: non-temporal (K/V bytes are read once)
-            pr.k[i][kk] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 2);
-            pr.v[i][kk] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 2);
-        }
 }
 
 // Per-segment merge scratch of the balanced kernel: the raw online-softmax state of every row
