@@ -403,6 +403,7 @@ BalArgs bal_args(const pdattn_plan* pl, const void* q, const void* k, const void
     a.Hkv = pl->Hkv;
     a.W = pl->W;
     a.scale_log2 = sm_scale * 1.4426950408889634f;
+    a.part_stride = 0;   // the planner's slot-major partials
     return a;
 }
 
@@ -731,13 +732,59 @@ int pdattn_plan_chunks(int G, int variant, int B, int Hkv, int max_len, int forc
     return PDATTN_OK;
 }
 
+// The uniform split's partial launch. Its items (pair, chunk) run on the balanced workgroup body,
+// several per workgroup so that the grid is about one workgroup per CU, with the segment
+// descriptors built in the kernel (so that the call needs only the device page table, as the
+// reference's does). A chunk spans at most ceil(chunk_tokens / 16) + 1 pages; one whose pages do
+// not fit the body's LDS page list (kRangeMax) runs on the one-chunk-per-workgroup kernel. With
+// `out` set (one chunk per sequence, nothing to merge), out / lse are written instead of partials.
+static int launch_uniform_split(const PartialArgs& a, int G, hipStream_t s) {
+    const int64_t ppi = ((int64_t)a.chunk_tokens + kPage - 1) / kPage + 1;
+    if (ppi > kRangeMax) {
+        PD_HIP(launch_decode_partial(a, G, s));
+        return PDATTN_OK;
+    }
+    DeviceFacts f;
+    if (int st = device_facts(&f)) return st;
+    const int64_t n_items = (int64_t)a.num_chunks * a.B * a.Hkv;
+    if (n_items > (int64_t)1 << 30) return fail(PDATTN_ERR_INVALID_ARGUMENT, "too many chunks");
+    int64_t per = (n_items + f.cus - 1) / f.cus;
+    per = std::max<int64_t>(1, std::min<int64_t>({per, (int64_t)kSegMax, kRangeMax / ppi}));
+    UniArgs u;
+    BalArgs& d = u.d;
+    d.q = a.q;
+    d.k = a.k;
+    d.v = a.v;
+    d.kv_indices = a.kv_indices;
+    d.out = a.out;
+    d.lse = a.lse;
+    d.desc = nullptr;
+    d.part_o = a.part_o;
+    d.part_lse = a.part_lse;
+    d.B = a.B;
+    d.Hq = a.Hq;
+    d.Hkv = a.Hkv;
+    d.W = (int)((n_items + per - 1) / per);
+    d.scale_log2 = a.scale_log2;
+    d.part_stride = a.part_stride;
+    u.kv_indptr = a.kv_indptr;
+    u.kv_last = a.kv_last;
+    u.kv_start = a.kv_start;
+    u.chunk_tokens = a.chunk_tokens;
+    u.num_chunks = a.num_chunks;
+    u.chunk_base = a.chunk_base;
+    u.n_items = (int)n_items;
+    u.per_wg = (int)per;
+    PD_HIP(launch_decode_uniform(u, G, s));
+    return PDATTN_OK;
+}
+
 int pdattn_decode_partial(const pdattn_decode_params* p, int G, int variant, void* stream) {
     if (variant < 0 || variant > 3) return fail(PDATTN_ERR_INVALID_ARGUMENT, "variant %d not in 0..3", variant);
     if (int st = check_decode_params(p, G)) return st;
     if (p->B == 0) return PDATTN_OK;
     if (!p->part_o || !p->part_lse) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null part_o / part_lse");
-    PD_HIP(launch_decode_partial(to_partial_args(p), G, static_cast<hipStream_t>(stream)));
-    return PDATTN_OK;
+    return launch_uniform_split(to_partial_args(p), G, static_cast<hipStream_t>(stream));
 }
 
 int pdattn_merge_states(const float* part_o, const float* part_lse, void* out, float* lse_out,
@@ -787,10 +834,9 @@ int pdattn_decode_attention(const pdattn_decode_params* p, int G, int variant, v
         // state returns it unchanged), and the merge launch is skipped
         a.out = static_cast<_Float16*>(out);
         a.lse = lse;
-        PD_HIP(launch_decode_partial(a, G, s));
-        return PDATTN_OK;
+        return launch_uniform_split(a, G, s);
     }
-    PD_HIP(launch_decode_partial(a, G, s));
+    if (int st = launch_uniform_split(a, G, s)) return st;
     PD_HIP(launch_merge_states(q.part_o, q.part_lse, static_cast<_Float16*>(out), lse, p->B * p->Hq,
                                p->part_stride, s));
     return PDATTN_OK;

@@ -662,8 +662,10 @@ __device__ __forceinline__ void flush_segment(BalSmem<C::G, C::NW * C::RPI>& sm,
             *reinterpret_cast<h4*>(a->out + (row0 + h) * kHeadDim + d0) = hv;
             if (d0 == 0) a->lse[row0 + h] = sm.lse[h];
         } else {
-            *reinterpret_cast<float4*>(a->part_o + ((size_t)slot * G + h) * kHeadDim + d0) = O;
-            if (d0 == 0) a->part_lse[(size_t)slot * G + h] = sm.lse[h];
+            const int ps = a->part_stride;
+            const size_t e = ps > 0 ? (row0 + h) * (size_t)ps + slot : (size_t)slot * G + h;
+            *reinterpret_cast<float4*>(a->part_o + e * kHeadDim + d0) = O;
+            if (d0 == 0) a->part_lse[e] = sm.lse[h];
         }
     }
     __syncthreads();   // sm is reused by the next segment
@@ -685,8 +687,9 @@ struct BalShared {
 
 // The body of one balanced-decode workgroup w (the kernel's argument block must start with the
 // BalArgs `a`, which kargs() reads).
-template <class C>
-__device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C>& S, int w) {
+template <class C, bool UNI = false>
+__device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C>& S, int w,
+                                              const UniArgs* u = nullptr) {
     constexpr int G = C::G, NW = C::NW, NT = C::NT, NBUF = C::NBUF, LPR = C::LPR;
     auto& sm = S.sm;
     int* pg = S.pg;
@@ -701,10 +704,45 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C>& S,
     // would count against the same wait counter as the ring's page loads, and a non-uniform value
     // in a buffer resource would turn every page load into a loop over lanes.
     auto fld = [&](int si, int f) { return __builtin_amdgcn_readfirstlane(sd[si * kSegInts + f]); };
-    const int32_t* desc = kargs()->desc + (size_t)w * kBalDescInts;
-    const int nseg = __builtin_amdgcn_readfirstlane(desc[0]);
-    if (nseg <= 0) return;   // uniform: the planner gives every workgroup at least one segment
-    for (int i = tid; i < nseg * kSegInts; i += NT) sd[i] = desc[8 + i];
+    int nseg;
+    if constexpr (!UNI) {
+        const int32_t* desc = kargs()->desc + (size_t)w * kBalDescInts;
+        nseg = __builtin_amdgcn_readfirstlane(desc[0]);
+        if (nseg <= 0) return;   // uniform: the planner gives every workgroup at least one segment
+        for (int i = tid; i < nseg * kSegInts; i += NT) sd[i] = desc[8 + i];
+    } else {
+        // items w, w + W, ...: thread t builds the descriptor of the t-th (the decode_partial
+        // rule, 01_decode_attention.cu:88-97: keys [kv_start + chunk * chunk_tokens, + chunk_tokens)
+        // clipped to the sequence; an empty range writes 0 / -inf). t0 is the first key of the
+        // range, which need not start a page: keys are numbered from its page's first token.
+        nseg = min(u->per_wg, (u->n_items - w + a.W - 1) / a.W);
+        if (nseg <= 0) return;   // uniform: the host sizes the grid so that every workgroup has items
+        if (tid < nseg) {
+            const int item = w + tid * a.W;
+            const int pair = item / u->num_chunks, chunk = item - pair * u->num_chunks;
+            const int b = pair / a.Hkv, kvh = pair - b * a.Hkv;
+            const int pb = u->kv_indptr[b], np = u->kv_indptr[b + 1] - pb;
+            const int len = np > 0 ? (np - 1) * kPage + u->kv_last[b] : 0;
+            const int kbeg = u->kv_start + chunk * u->chunk_tokens;
+            const int kend = max(kbeg, min(len, kbeg + u->chunk_tokens));
+            const int pf = kbeg / kPage;
+            int* sg = sd + tid * kSegInts;
+            sg[0] = b;
+            sg[1] = kvh;
+            sg[3] = kend > kbeg ? (kend - 1) / kPage - pf + 1 : 0;
+            sg[4] = kbeg;
+            sg[5] = kend;
+            sg[6] = pb + pf;
+            sg[7] = a.out != nullptr ? -1 : u->chunk_base + chunk;
+        }
+        __syncthreads();
+        // page-list offsets: exclusive prefix sum of the page counts
+        if (tid < nseg) {
+            int qa = 0;
+            for (int j = 0; j < tid; ++j) qa += sd[j * kSegInts + 3];
+            sd[tid * kSegInts + 2] = qa;
+        }
+    }
     __syncthreads();
     // page ids and q rows of every segment into LDS: all loads are issued before any is stored
     // (one round trip, not one per segment). Item i < npages is page i of the workgroup's list,
@@ -787,6 +825,7 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C>& S,
     reset_state<C>(st);
     for (int si = 0; si < nseg; ++si) {
         const int npg = fld(si, 3), t0 = fld(si, 4), t1 = fld(si, 5);
+        const int tbase = t0 & ~(kPage - 1);   // first token of the segment's first page
         f16x2 qv[G][C::PPL][4];
 #pragma unroll
         for (int h = 0; h < G; ++h)
@@ -802,7 +841,7 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C>& S,
             for (int u = 0; u < NBUF; ++u) {
                 issue(buf[(u + NBUF - 1) % NBUF]);
                 if (blk + u < cnt)
-                    page_step<C>(st, buf[u], qv, t0 + (wave + NW * (blk + u)) * kPage + r, t0, t1,
+                    page_step<C>(st, buf[u], qv, tbase + (wave + NW * (blk + u)) * kPage + r, t0, t1,
                                  a.scale_log2);
             }
         }
@@ -815,6 +854,14 @@ template <class C>
 __global__ __launch_bounds__(C::NT) void decode_balanced_kernel(BalArgs a) {
     __shared__ BalShared<C> S;
     balanced_body<C>(a, S, blockIdx.x);
+}
+
+// The reference-shaped uniform split on the balanced body (items of equal key ranges, descriptors
+// built in the kernel from the device page table).
+template <class C>
+__global__ __launch_bounds__(C::NT) void decode_uniform_kernel(UniArgs u) {
+    __shared__ BalShared<C> S;
+    balanced_body<C, true>(u.d, S, blockIdx.x, &u);
 }
 
 // The fused cascade step: blocks [0, n_dec) are the suffix decode's workgroups, the rest the
@@ -878,6 +925,10 @@ void launch_b(const BalArgs& a, hipStream_t s) {
     decode_balanced_kernel<C><<<a.W, C::NT, 0, s>>>(a);
 }
 template <class C>
+void launch_u(const UniArgs& a, hipStream_t s) {
+    decode_uniform_kernel<C><<<a.d.W, C::NT, 0, s>>>(a);
+}
+template <class C>
 void launch_step(const StepArgs& a, hipStream_t s) {
     cascade_step_kernel<C><<<a.n_dec + a.n_pre, C::NT, 0, s>>>(a);
 }
@@ -922,6 +973,13 @@ hipError_t launch_merge_states(const float* part_o, const float* part_lse, _Floa
 hipError_t launch_decode_balanced(const BalArgs& a, int G, hipStream_t s) {
     if (G != 1 && G != 2 && G != 4 && G != 8) return hipErrorInvalidValue;
     PD_DISPATCH(BalCfg, G, launch_b, a, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_uniform(const UniArgs& a, int G, hipStream_t s) {
+    if (G != 1 && G != 2 && G != 4 && G != 8) return hipErrorInvalidValue;
+    if (a.d.W <= 0) return hipSuccess;
+    PD_DISPATCH(BalCfg, G, launch_u, a, s);
     return hipGetLastError();
 }
 

@@ -56,6 +56,23 @@ struct BalArgs {
     float*          part_lse;     // [slots * G]
     int B, Hq, Hkv, W;
     float scale_log2;             // sm_scale * log2(e)
+    // Partial layout: 0 = slot-major (head h of slot s at s * G + h, the planner's slots); > 0 =
+    // row-major with this stride (row r = b * Hq + h, slot s at r * part_stride + s: the layout of
+    // the reference's decode_partial, where s = chunk_base + chunk)
+    int part_stride;
+};
+
+// The reference-shaped uniform split (decode_partial / decode_attention) run by the balanced
+// workgroup body: item i = (pair, chunk) with chunk = i % num_chunks, pair = b * Hkv + kvh =
+// i / num_chunks covers keys [kv_start + chunk * chunk_tokens, + chunk_tokens) of its sequence.
+// Workgroup w of d.W takes the items w, w + W, ... (at most per_wg of them) and builds their
+// segment descriptors itself from the device page table, so no host plan is involved. The
+// BalArgs come first: the body reads them through the kernel argument pointer.
+struct UniArgs {
+    BalArgs         d;            // d.kv_indices is not offset; d.out != null: write out / lse
+    const int32_t*  kv_indptr;
+    const int32_t*  kv_last;
+    int kv_start, chunk_tokens, num_chunks, chunk_base, n_items, per_wg;
 };
 
 // Merge of split pairs (and of every pair when extra partials are given): entry e of `list` is
@@ -120,6 +137,7 @@ hipError_t launch_decode_partial(const PartialArgs& a, int G, hipStream_t s);
 hipError_t launch_merge_states(const float* part_o, const float* part_lse, _Float16* out,
                                float* lse, int rows, int num_chunks, hipStream_t s);
 hipError_t launch_decode_balanced(const BalArgs& a, int G, hipStream_t s);
+hipError_t launch_decode_uniform(const UniArgs& a, int G, hipStream_t s);
 hipError_t launch_merge_split(const MergeArgs& a, int n_entries, hipStream_t s);
 hipError_t launch_fill_i32(int32_t* p, int32_t value, size_t n, hipStream_t s);
 hipError_t launch_cascade_prefix(const PrefixArgs& a, int G, int qtiles, hipStream_t s);

@@ -89,6 +89,46 @@ def test_uniform_kv_start_matches_oracle():
         check_lse(l, rl, tag=f"kv_start={kv_start}")
 
 
+UNIFORM_SHAPES = [
+    # tag, lens, Hq, Hkv, num_chunks, chunk_tokens, kv_start
+    ("chunk past the LDS page list", [40000, 123], 32, 8, 1, 40000, 0),   # 2501 pages: one-chunk kernel
+    ("long chunks", [40000, 123], 32, 8, 2, 20000, 0),
+    ("many items per workgroup", "ragged300", 8, 8, 1, 304, 0),         # 2400 items, 10 per workgroup
+    ("segment cap per workgroup", "ragged300", 8, 8, 3, 100, 0),        # 7200 items, 24 per workgroup
+    ("unaligned start and chunk", [1000, 77, 0, 513], 32, 8, 5, 200, 23),
+]
+
+
+@pytest.mark.parametrize("case", UNIFORM_SHAPES, ids=[c[0] for c in UNIFORM_SHAPES])
+def test_uniform_items_per_workgroup(case):
+    """The reference-shaped split runs several (pair, chunk) items per workgroup on the balanced
+    body, with descriptors built in the kernel: items per workgroup up to the segment cap, empty
+    sequences among them, chunks that do not start or end on a page, and a chunk too long for the
+    LDS page list (the one-chunk-per-workgroup kernel). Final out / lse and the partials."""
+    import _gpu
+    import pdattn
+    tag, lens, Hq, Hkv, nc, ct, kv_start = case
+    if lens == "ragged300":
+        lens = [int(x) for x in np.random.default_rng(3).integers(0, 301, 300)]
+    print(f"[case] {tag} B={len(lens)} max_len={max(lens)} nc={nc} ct={ct} kv_start={kv_start}", flush=True)
+    bt = inputs.make_batch(lens, Hq, Hkv, seed=29)
+    db = _gpu.DeviceBatch(bt)
+    p = db.params(nc, ct, kv_start=kv_start)
+    ws = pdattn.Workspace()
+    pdattn.decode_attention(p, bt.G, db.out, db.lse, ws)
+    o, l = db.results()
+    pdattn.workspace_release(ws)
+    ro, rl = _ref(bt, kv_start)
+    check_out(o, ro, tag=tag)
+    check_lse(l, rl, tag=tag)
+    if bt.B * bt.Hq * nc <= 20000:
+        po, pl = _gpu.run_partials(db, nc, ct, kv_start)
+        pro, prl = oracle.partials(bt.q, bt.k, bt.v, bt.indptr, bt.indices, bt.last, bt.Hq, bt.Hkv,
+                                   nc, ct, kv_start)
+        check_lse(pl, prl, tag=tag + " part_lse")
+        check_out(po, pro, tag=tag + " part_o")
+
+
 @pytest.mark.parametrize("kv_start", [0, 40])
 def test_single_chunk_skips_the_merge_bitwise(kv_start):
     """decode_attention with one chunk per sequence writes out / lse from the partial kernel:
