@@ -12,7 +12,7 @@
 // Computing the transposed products puts one query per lane column of every 16x16 accumulator
 // (lane l holds rows 4*(l/16)+j, column l%16), so
 //   * the running max / sum of a query live in the lanes of that column: a row max over a key
-//     tile is an in-lane max plus two cross-lane steps, and the rescale of the output
+//     tile is an in-lane max plus two VALU lane swaps (col4_reduce), and the rescale of the output
 //     accumulator by exp(m_old - m_new) is a per-lane scalar multiply;
 //   * P leaves the S^T accumulator already in the B-operand layout of the PV product (the 8
 //     keys a lane contributes are 4 of one 16-key tile and 4 of the next; V^T is read with the
