@@ -469,7 +469,7 @@ __global__ __launch_bounds__(C::NT) void decode_partial_kernel(PartialArgs a) {
     const int b = blockIdx.y / a.Hkv, kvh = blockIdx.y % a.Hkv;
     const int pb = a.kv_indptr[b];
     const int np = a.kv_indptr[b + 1] - pb;
-    const int len = np > 0 ? (np - 1) * kPage + a.kv_last[b] : 0;
+    const int len = np > 0 ? (np - 1) * kPage + min(kPage, max(1, a.kv_last[b])) : 0;
     const int kbeg = a.kv_start + chunk * a.chunk_tokens;
     const int kend = min(len, kbeg + a.chunk_tokens);
     process_range<C>(sm, a.q + ((size_t)b * a.Hq + kvh * G) * kHeadDim, a.k, a.v,
@@ -722,7 +722,8 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C>& S,
             const int pair = item / u->num_chunks, chunk = item - pair * u->num_chunks;
             const int b = pair / a.Hkv, kvh = pair - b * a.Hkv;
             const int pb = u->kv_indptr[b], np = u->kv_indptr[b + 1] - pb;
-            const int len = np > 0 ? (np - 1) * kPage + u->kv_last[b] : 0;
+            // (a last-page length outside [1, 16] is clamped: no key past the sequence's pages)
+            const int len = np > 0 ? (np - 1) * kPage + min(kPage, max(1, u->kv_last[b])) : 0;
             const int kbeg = u->kv_start + chunk * u->chunk_tokens;
             const int kend = max(kbeg, min(len, kbeg + u->chunk_tokens));
             const int pf = kbeg / kPage;
