@@ -6,10 +6,12 @@
 // as a normalized partial (o, lse), then a log-sum-exp merge of the partials.
 //
 // How it maps to CDNA4:
-//  * Two workgroup shapes. The uniform split (decode_partial_kernel, the reference's launch
-//    shape) is 8 waves on one (sequence, kv head, chunk), each wave on every 8th page. The
-//    balanced decode (decode_balanced_kernel, the plan/run path) is 4 waves, one per SIMD and one
-//    workgroup per CU, walking a planned list of segments, each wave on every 4th page.
+//  * One workgroup body (balanced_body): 4 waves, one per SIMD and one workgroup per CU, walking
+//    a list of segments (pieces of one sequence and kv head), each wave on every 4th page, with
+//    one page ring across all of them. The plan/run path (decode_balanced_kernel) reads the list
+//    from a host-built plan; the reference-shaped uniform split (decode_uniform_kernel) builds it
+//    in the kernel from the device page table. A uniform chunk too long for the body's LDS page
+//    list runs on decode_partial_kernel, one workgroup per (sequence, kv head, chunk).
 //  * K and V rows go straight from HBM into VGPRs with 16-byte non-temporal loads: a 256-byte
 //    row (128 fp16) is read by LPR lanes, so one wave-wide load instruction reads 64/LPR rows of
 //    one page, each as whole 128-byte lines. No LDS staging is needed because every lane reads
@@ -27,11 +29,9 @@
 //  * Prefetch: a two-page ring in VGPRs; the loads of the next page are issued before the
 //    current page is computed.
 //
-// Lane geometry, G = query heads per kv head:
-//   uniform split, G <= 4: LPR = 8 lanes per row, 8 rows per load, each lane holds 2 rows x 16
-//           dims of a page;
-//   uniform split at G == 8, and the balanced decode: LPR = 16, 4 rows per load, each lane holds
-//           4 rows x 8 dims (keeps the fp32 output state at 64 VGPRs at G = 8).
+// Lane geometry (both kernels), G = query heads per kv head: LPR = 16 lanes per 256-byte K/V row,
+// 4 rows per wave-wide load, each lane holding 4 rows x 8 dims of a page (keeps the fp32 output
+// state at 64 VGPRs at G = 8).
 // Lane (r = lane / LPR, c = lane % LPR) holds rows i*RPI + r of each page and the 16-byte pieces
 // kk*LPR + c (dims 8*(kk*LPR + c) .. +7), kk < PPL.
 #include <math.h>
@@ -892,30 +892,20 @@ int occupancy_of(const void* fn, int threads) {
 }
 
 // Kernel shapes per group size G.
-// Uniform split (reference launch shape): 16 lanes per 256-byte row, 4 waves, a two-page ring.
-// Against 8 lanes per row and 8 waves (the planner then picks half the chunks, by occupancy),
-// measured cold: 64x1K 57.0 vs 64.3 us, 1x32K 39.9 vs 39.8 us, 8x8K 57.2 vs 57.8 us.
-#ifndef PD_PART_LPR
-#define PD_PART_LPR 16
-#endif
-#ifndef PD_PART_NW
-#define PD_PART_NW 4
-#endif
+// One-chunk-per-workgroup kernel (the uniform split's fallback for chunks past the LDS page list):
+// 16 lanes per 256-byte row, 4 waves, a two-page ring. Against 8 lanes per row and 8 waves (the
+// planner then picks half the chunks, by occupancy), measured cold when it ran every uniform
+// split: 64x1K 57.0 vs 64.3 us, 1x32K 39.9 vs 39.8 us, 8x8K 57.2 vs 57.8 us.
 template <int G>
-using PartialCfg = Cfg<G, (G >= 8 ? 16 : PD_PART_LPR), PD_PART_NW, 2>;
-// Balanced launch: 4 waves (one per SIMD, one workgroup per CU), 16 lanes per row (four row groups
-// per wave, so the end-of-segment merge is two permlane steps), a two-page ring: one page in
-// flight while the other is computed. Deeper rings measured slower at every shape (4 pages:
-// 30.6 vs 28.5 us back to back at 1x32K, 46.1 vs 44.9 us at 64x1K; at G = 8, 3 pages: 29.3 vs
-// 28.6 us and 42.8 vs 41.4 us): more bytes in flight only lengthen the memory queues.
-#ifndef PD_BAL_NBUF
-#define PD_BAL_NBUF 2
-#endif
-#ifndef PD_BAL_NBUF8
-#define PD_BAL_NBUF8 2
-#endif
+using PartialCfg = Cfg<G, 16, 4, 2>;
+// Balanced body (plan/run, the uniform split and the cascade's suffix): 4 waves (one per SIMD,
+// one workgroup per CU), 16 lanes per row (four row groups per wave, so the end-of-segment merge
+// is two permlane steps), a two-page ring: one page in flight while the other is computed. Deeper
+// rings measured slower at every shape (4 pages: 30.6 vs 28.5 us back to back at 1x32K, 46.1 vs
+// 44.9 us at 64x1K; at G = 8, 3 pages: 29.3 vs 28.6 us and 42.8 vs 41.4 us): more bytes in
+// flight only lengthen the memory queues.
 template <int G>
-using BalCfg = Cfg<G, 16, 4, (G >= 8 ? PD_BAL_NBUF8 : PD_BAL_NBUF)>;
+using BalCfg = Cfg<G, 16, 4, 2>;
 
 template <class C>
 void launch_p(const PartialArgs& a, hipStream_t s) {

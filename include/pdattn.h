@@ -98,8 +98,10 @@ void pdattn_workspace_release(pdattn_workspace* ws);
 int pdattn_plan_chunks(int G, int variant, int B, int Hkv, int max_len, int force_chunks,
                        int* num_chunks, int* chunk_tokens);
 
-/* Partial (o, lse) per chunk into p->part_o / p->part_lse; grid (num_chunks, B*Hkv)
- * (decode_partial<G,V>, 01_decode_attention.cu:76-236, launched at 01:327-329). */
+/* Partial (o, lse) per chunk into p->part_o / p->part_lse, slot chunk_base + chunk of each row
+ * at stride part_stride (decode_partial<G,V>, 01_decode_attention.cu:76-236, launched at
+ * 01:327-329). The (chunk, sequence, kv head) items run several per workgroup, about one workgroup
+ * per CU; chunks longer than 32752 tokens run one per workgroup. Reads only the device page table. */
 int pdattn_decode_partial(const pdattn_decode_params* p, int G, int variant, void* stream);
 
 /* Log-sum-exp merge of `num_chunks` partial states for each of `rows` rows into fp16 out and
