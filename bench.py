@@ -39,8 +39,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
-    ap.add_argument("--only", default="", choices=["", "32k", "64x1k", "cascade", "prefix", "append", "graph",
-                                                   "tree"],
+    ap.add_argument("--only", default="", choices=["", "32k", "64x1k", "cascade", "cascade8", "prefix", "append",
+                                                   "graph", "tree"],
                     help="run one workload only (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only torch copies of COPY_BYTES (known-size traffic for counter runs)")
@@ -300,14 +300,16 @@ def gbs(nbytes, seconds):
     return nbytes / seconds / 1e9
 
 
-def cascade_workload(timer, args):
-    """64 requests x (8192 shared + 512 private): cascade vs the non-shared kernel, same method."""
+def cascade_workload(timer, args, Hq=32, Hkv=8):
+    """64 requests x (8192 shared + 512 private): cascade vs the non-shared kernel, same method.
+    Hq=32, Hkv=8 is BASELINE configs[4]; Hq=64, Hkv=8 (G=8) is the same batch with twice the query
+    heads per kv head."""
     import pdattn
     s = timer.stream
-    bt3, t3 = make_device_batch(None, 32, 8, seed=21, shared_prefix=8192, suffix=[512] * 64)
+    bt3, t3 = make_device_batch(None, Hq, Hkv, seed=21, shared_prefix=8192, suffix=[512] * 64)
     f3n, plan3, ws3 = streamk_runner(bt3, t3, s)
     base = pdattn.make_params(t3["q"], t3["k"], t3["v"], t3["indptr"], t3["indices"], t3["last"],
-                              bt3.B, 32, 8)
+                              bt3.B, Hq, Hkv)
     cp = pdattn.CascadePlan(base, bt3.indptr, bt3.indices, bt3.lens, t3["indices"])
     cws = pdattn.Workspace()
     cp.decode(t3["out"], t3["lse"], cws, s)  # uploads the schedule
@@ -535,6 +537,9 @@ def main():
     if args.only == "cascade":
         print(json.dumps({"cascade_64x(8192+512)": cascade_workload(timer, args)}))
         return
+    if args.only == "cascade8":
+        print(json.dumps({"cascade_64x(8192+512)_G8": cascade_workload(timer, args, 64, 8)}))
+        return
     if args.only == "prefix":
         print(json.dumps({"cascade_prefix_mfma": prefix_workload(timer, args)}))
         return
@@ -599,6 +604,7 @@ def main():
                         "workgroups": h2["workgroups"], "algorithmic_bytes": h2["bytes"],
                         "uniform_path": h2["uniform"]}
         sec["cascade_64x(8192+512)"] = cascade_workload(timer, args)
+        sec["cascade_64x(8192+512)_G8"] = cascade_workload(timer, args, 64, 8)
         sec["cascade_prefix_mfma"] = prefix_workload(timer, args)
         sec["append_kv"] = append_workload(timer, args)
         sec["hip_graph"] = graph_workload(timer, args)

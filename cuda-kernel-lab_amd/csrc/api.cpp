@@ -225,10 +225,11 @@ namespace {
 // [U w / W, U (w+1) / W) of that order; the walk below cuts each range into one segment per chunk
 // piece. The contributors of a pair are its segments in unit order; a pair with more than one
 // (or every pair, when `merge_all` is set for extra partials) gets consecutive partial slots and
-// an entry in the merge list. W grows (doubling) until every workgroup has at most kSegMax
-// segments and kRangeMax pages.
+// an entry in the merge list. W grows (doubling) until every workgroup has at most seg_cap
+// (<= kSegMax) segments and kRangeMax pages.
 int build_balanced_plan(const int32_t* indptr, const int32_t* last, int B, int Hq, int Hkv,
-                        int force_wg, int chunk_pages, bool merge_all, pdattn_plan* pl) {
+                        int force_wg, int chunk_pages, bool merge_all, pdattn_plan* pl,
+                        int seg_cap = kSegMax) {
     int G = 0;
     if (int st = check_heads(Hq, Hkv, &G)) return st;
     if (B < 0) return fail(PDATTN_ERR_INVALID_ARGUMENT, "B=%d is negative", B);
@@ -287,7 +288,7 @@ int build_balanced_plan(const int32_t* indptr, const int32_t* last, int B, int H
                         if (wend - wbeg > kRangeMax) { ok = false; break; }
                         const int take = (int)std::min<int64_t>(pn - done, wend - u);
                         int32_t* d = &desc[(size_t)w * kBalDescInts];
-                        if (d[0] == kSegMax) { ok = false; break; }
+                        if (d[0] == seg_cap) { ok = false; break; }
                         int32_t* sg = d + 8 + kSegInts * d[0];
                         const int p0 = pa + done, p1 = pa + done + take;
                         sg[0] = b;
@@ -571,7 +572,9 @@ int cascade_plan_create(const pdattn_decode_params* base, const int32_t* h_indpt
             for (int i = h_indptr[b] + start[b]; i < h_indptr[b + 1]; ++i) sidx.push_back(h_indices[i]);
             sind[b + 1] = (int32_t)sidx.size();
         }
-        st = build_balanced_plan(sind.data(), last.data(), B, base->Hq, base->Hkv, 0, 0, true, &cp->sk);
+        // at G = 8 the fused step's decode role stages q rows for at most kStepSegMax segments
+        st = build_balanced_plan(sind.data(), last.data(), B, base->Hq, base->Hkv, 0, 0, true, &cp->sk,
+                                 G > 4 ? kStepSegMax : kSegMax);
         // The prefix work of every node goes into one launch (nodes of different depths write
         // different partial columns, so they are independent). Fused step (default where two of
         // its workgroups fit on a CU): about one prefix workgroup per CU, beside the suffix

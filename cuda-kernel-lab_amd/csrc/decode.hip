@@ -538,13 +538,13 @@ __global__ __launch_bounds__(kMergeThreads) void merge_split_kernel(MergeArgs a)
 // Per-segment merge scratch of the balanced kernel: the raw online-softmax state of every row
 // group of every wave (NS = waves x row groups sources), then per-source weights. o rows are
 // padded by 4 floats so that the row groups of a wave, which write the same columns, fall in
-// different LDS banks.
-template <int G, int NS>
+// different LDS banks. The o rows hold HP of the G heads at a time (the flush takes G / HP passes).
+template <int G, int NS, int HP = G>
 struct BalSmem {
     static constexpr int OP = kHeadDim + 4;
     float m[NS][G];
     float l[NS][G];
-    float o[NS][G][OP];
+    float o[NS][HP][OP];
     float alpha[G][NS];       // exp(m_src - M) per head and source
     float rinv[G];            // 1 / L
     float lse[G];
@@ -581,94 +581,101 @@ __device__ __forceinline__ float class_reduce(float v) {
 // End of a segment. Every row group of every wave is one source state (max, sum, output slice);
 // all of them go to LDS unmerged, one wave turns the per-source maxima into weights, and each
 // thread forms four outputs as one weighted sum over the sources, in source order. Writes the G
-// rows as the final fp16 out / lse (slot < 0) or as partial slot `slot` (normalized o, lse).
-template <class C>
-__device__ __forceinline__ void flush_segment(BalSmem<C::G, C::NW * C::RPI>& sm, WaveState<C>& st,
+// rows as the final fp16 out / lse (slot < 0) or as partial slot `slot` (normalized o, lse). The
+// raw outputs go through LDS HP heads at a time (HP = G: one pass).
+template <class C, int HP>
+__device__ __forceinline__ void flush_segment(BalSmem<C::G, C::NW * C::RPI, HP>& sm, WaveState<C>& st,
                                               KArgPtr a, size_t row0, int slot) {
     constexpr int G = C::G, LPR = C::LPR, NS = C::NW * C::RPI;
     // one wave computes the source weights: lane = s * G + h covers sources s + j * SL, j < J
     constexpr int SL = 64 / G, J = (NS + SL - 1) / SL;
-    static_assert(NS % 4 == 0 && G * 32 <= C::NT, "float4 passes");
+    static_assert(NS % 4 == 0 && HP * 32 <= C::NT && G % HP == 0, "float4 passes");
     const int tid = threadIdx.x, lane = tid & 63, c = lane % LPR;
     const int src = (tid >> 6) * C::RPI + lane / LPR;
 #pragma unroll
-    for (int h = 0; h < G; ++h)
+    for (int hp = 0; hp < G / HP; ++hp) {
 #pragma unroll
-        for (int kk = 0; kk < C::PPL; ++kk) {
-            float4* dst = reinterpret_cast<float4*>(&sm.o[src][h][(kk * LPR + c) * 8]);
-            dst[0] = make_float4(st.o[h][kk * 8 + 0], st.o[h][kk * 8 + 1], st.o[h][kk * 8 + 2], st.o[h][kk * 8 + 3]);
-            dst[1] = make_float4(st.o[h][kk * 8 + 4], st.o[h][kk * 8 + 5], st.o[h][kk * 8 + 6], st.o[h][kk * 8 + 7]);
-        }
-    if (c == 0) {
+        for (int hh = 0; hh < HP; ++hh)
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-            sm.m[src][h] = st.m[h];
-            sm.l[src][h] = st.l[h];
-        }
-    }
-    __syncthreads();
-    if (tid < 64) {
-        const int s0 = tid / G, h = tid % G;
-        float mv[J];
-        float M = -INFINITY;
+            for (int kk = 0; kk < C::PPL; ++kk) {
+                const int h = hp * HP + hh;
+                float4* dst = reinterpret_cast<float4*>(&sm.o[src][hh][(kk * LPR + c) * 8]);
+                dst[0] = make_float4(st.o[h][kk * 8 + 0], st.o[h][kk * 8 + 1], st.o[h][kk * 8 + 2], st.o[h][kk * 8 + 3]);
+                dst[1] = make_float4(st.o[h][kk * 8 + 4], st.o[h][kk * 8 + 5], st.o[h][kk * 8 + 6], st.o[h][kk * 8 + 7]);
+            }
+        if (hp == 0 && c == 0) {
 #pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const int s = s0 + j * SL;
-            mv[j] = s < NS ? sm.m[s][h] : -INFINITY;
-            M = fmaxf(M, mv[j]);
-        }
-        M = class_reduce<G, true>(M);
-        float L = 0.f;
-#pragma unroll
-        for (int j = 0; j < J; ++j) {
-            const int s = s0 + j * SL;
-            const float al = (mv[j] == -INFINITY) ? 0.f : fast_exp2(mv[j] - M);
-            if (s < NS) {
-                sm.alpha[h][s] = al;
-                L = fmaf(al, sm.l[s][h], L);
+            for (int h = 0; h < G; ++h) {
+                sm.m[src][h] = st.m[h];
+                sm.l[src][h] = st.l[h];
             }
         }
-        L = class_reduce<G, false>(L);
-        if (tid < G) {
-            sm.rinv[h] = L > 0.f ? 1.f / L : 0.f;
-            sm.lse[h] = L > 0.f ? (M + fast_log2(L)) * kLn2 : -INFINITY;
+        __syncthreads();
+        if (hp == 0) {
+            if (tid < 64) {
+                const int s0 = tid / G, h = tid % G;
+                float mv[J];
+                float M = -INFINITY;
+#pragma unroll
+                for (int j = 0; j < J; ++j) {
+                    const int s = s0 + j * SL;
+                    mv[j] = s < NS ? sm.m[s][h] : -INFINITY;
+                    M = fmaxf(M, mv[j]);
+                }
+                M = class_reduce<G, true>(M);
+                float L = 0.f;
+#pragma unroll
+                for (int j = 0; j < J; ++j) {
+                    const int s = s0 + j * SL;
+                    const float al = (mv[j] == -INFINITY) ? 0.f : fast_exp2(mv[j] - M);
+                    if (s < NS) {
+                        sm.alpha[h][s] = al;
+                        L = fmaf(al, sm.l[s][h], L);
+                    }
+                }
+                L = class_reduce<G, false>(L);
+                if (tid < G) {
+                    sm.rinv[h] = L > 0.f ? 1.f / L : 0.f;
+                    sm.lse[h] = L > 0.f ? (M + fast_log2(L)) * kLn2 : -INFINITY;
+                }
+            }
+            __syncthreads();
         }
-    }
-    __syncthreads();
-    if (tid < G * 32) {
-        const int h = tid / 32, d0 = 4 * (tid % 32);
-        float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (tid < HP * 32) {
+            const int hh = tid / 32, h = hp * HP + hh, d0 = 4 * (tid % 32);
+            float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int s4 = 0; s4 < NS; s4 += 4) {
-            const float4 al = *reinterpret_cast<const float4*>(&sm.alpha[h][s4]);
-            const float alv[4] = {al.x, al.y, al.z, al.w};
+            for (int s4 = 0; s4 < NS; s4 += 4) {
+                const float4 al = *reinterpret_cast<const float4*>(&sm.alpha[h][s4]);
+                const float alv[4] = {al.x, al.y, al.z, al.w};
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float4 ov = *reinterpret_cast<const float4*>(&sm.o[s4 + u][h][d0]);
-                O.x = fmaf(alv[u], ov.x, O.x);
-                O.y = fmaf(alv[u], ov.y, O.y);
-                O.z = fmaf(alv[u], ov.z, O.z);
-                O.w = fmaf(alv[u], ov.w, O.w);
+                for (int u = 0; u < 4; ++u) {
+                    const float4 ov = *reinterpret_cast<const float4*>(&sm.o[s4 + u][hh][d0]);
+                    O.x = fmaf(alv[u], ov.x, O.x);
+                    O.y = fmaf(alv[u], ov.y, O.y);
+                    O.z = fmaf(alv[u], ov.z, O.z);
+                    O.w = fmaf(alv[u], ov.w, O.w);
+                }
+            }
+            const float ri = sm.rinv[h];
+            O.x *= ri;
+            O.y *= ri;
+            O.z *= ri;
+            O.w *= ri;
+            if (slot < 0) {
+                typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+                const h4 hv = {(_Float16)O.x, (_Float16)O.y, (_Float16)O.z, (_Float16)O.w};
+                *reinterpret_cast<h4*>(a->out + (row0 + h) * kHeadDim + d0) = hv;
+                if (d0 == 0) a->lse[row0 + h] = sm.lse[h];
+            } else {
+                const int ps = a->part_stride;
+                const size_t e = ps > 0 ? (row0 + h) * (size_t)ps + slot : (size_t)slot * G + h;
+                *reinterpret_cast<float4*>(a->part_o + e * kHeadDim + d0) = O;
+                if (d0 == 0) a->part_lse[e] = sm.lse[h];
             }
         }
-        const float ri = sm.rinv[h];
-        O.x *= ri;
-        O.y *= ri;
-        O.z *= ri;
-        O.w *= ri;
-        if (slot < 0) {
-            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-            const h4 hv = {(_Float16)O.x, (_Float16)O.y, (_Float16)O.z, (_Float16)O.w};
-            *reinterpret_cast<h4*>(a->out + (row0 + h) * kHeadDim + d0) = hv;
-            if (d0 == 0) a->lse[row0 + h] = sm.lse[h];
-        } else {
-            const int ps = a->part_stride;
-            const size_t e = ps > 0 ? (row0 + h) * (size_t)ps + slot : (size_t)slot * G + h;
-            *reinterpret_cast<float4*>(a->part_o + e * kHeadDim + d0) = O;
-            if (d0 == 0) a->part_lse[e] = sm.lse[h];
-        }
+        __syncthreads();   // sm is reused by the next pass or segment
     }
-    __syncthreads();   // sm is reused by the next segment
 }
 
 // One workgroup of 4 waves (one per SIMD) per CU walks its list of segments. Wave i takes pages
@@ -677,18 +684,23 @@ __device__ __forceinline__ void flush_segment(BalSmem<C::G, C::NW * C::RPI>& sm,
 // time. The ring runs across segment boundaries: the next segment's first pages are in flight
 // while a segment is flushed. Partials are written with plain stores and merged by a second
 // kernel, so no workgroup waits for another.
-template <class C>
+// COMPACT (the fused cascade step at G = 8, so that a CU holds it beside a prefix workgroup):
+// the flush passes 4 heads at a time, and q rows are staged for at most kStepSegMax segments (the
+// planner caps such a plan's segments per workgroup).
+template <class C, bool COMPACT = false>
 struct BalShared {
-    BalSmem<C::G, C::NW * C::RPI> sm;
+    static constexpr int HP = COMPACT && C::G > 4 ? 4 : C::G;        // heads per flush pass
+    static constexpr int SEGS = COMPACT ? kStepSegMax : kSegMax;      // segments with staged q rows
+    BalSmem<C::G, C::NW * C::RPI, HP> sm;
     int pg[kRangeMax];                             // the workgroup's page ids
-    u32x4 qs[kSegMax][C::G * kHeadDim / 8];        // q rows of each segment
+    u32x4 qs[SEGS][C::G * kHeadDim / 8];           // q rows of each segment
     int sd[kSegMax * kSegInts];                    // segment descriptors
 };
 
 // The body of one balanced-decode workgroup w (the kernel's argument block must start with the
 // BalArgs `a`, which kargs() reads).
-template <class C, bool UNI = false>
-__device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C>& S, int w,
+template <class C, bool UNI = false, bool COMPACT = false>
+__device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COMPACT>& S, int w,
                                               const UniArgs* u = nullptr) {
     constexpr int G = C::G, NW = C::NW, NT = C::NT, NBUF = C::NBUF, LPR = C::LPR;
     auto& sm = S.sm;
@@ -750,7 +762,8 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C>& S,
     // found in the segment whose range [qa, qa + npg) holds it; q item j is 16 bytes of the
     // G q rows of segment j / (G*16).
     {
-        constexpr int PMAX = kRangeMax / NT, QPS = G * kHeadDim / 8, QMAX = (kSegMax * QPS + NT - 1) / NT;
+        constexpr int PMAX = kRangeMax / NT, QPS = G * kHeadDim / 8;
+        constexpr int QMAX = (BalShared<C, COMPACT>::SEGS * QPS + NT - 1) / NT;
         const int npages = fld(nseg - 1, 2) + fld(nseg - 1, 3);
         int pv[PMAX];
         u32x4 qv4[QMAX];
@@ -846,7 +859,9 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C>& S,
                                  a.scale_log2);
             }
         }
-        flush_segment<C>(sm, st, kargs(), (size_t)fld(si, 0) * a.Hq + (size_t)fld(si, 1) * G, fld(si, 7));
+        flush_segment<C, BalShared<C, COMPACT>::HP>(sm, st, kargs(),
+                                                    (size_t)fld(si, 0) * a.Hq + (size_t)fld(si, 1) * G,
+                                                    fld(si, 7));
         reset_state<C>(st);
     }
 }
@@ -874,11 +889,12 @@ __global__ __launch_bounds__(C::NT) void decode_uniform_kernel(UniArgs u) {
 template <class C>
 __global__ __launch_bounds__(C::NT, 2) void cascade_step_kernel(StepArgs s) {
     static_assert(C::NT == kPrefixThreads, "both roles use the same workgroup shape");
-    constexpr size_t SB = sizeof(BalShared<C>) > sizeof(PSmem) ? sizeof(BalShared<C>) : sizeof(PSmem);
+    typedef BalShared<C, (C::G > 4)> Dec;   // G = 8: the compact layout (fits beside a prefix workgroup)
+    constexpr size_t SB = sizeof(Dec) > sizeof(PSmem) ? sizeof(Dec) : sizeof(PSmem);
     __shared__ __align__(16) unsigned char raw[SB];
     const int i = blockIdx.x;
     if (i < s.n_dec) {
-        balanced_body<C>(s.d, *reinterpret_cast<BalShared<C>*>(raw), i);
+        balanced_body<C, false, (C::G > 4)>(s.d, *reinterpret_cast<Dec*>(raw), i);
     } else {
         const int j = i - s.n_dec, n_items = s.p.num_chunks;
         prefix_workgroup(s.p, *reinterpret_cast<PSmem*>(raw), j % n_items, 0, j / n_items);

@@ -40,6 +40,7 @@ struct PartialArgs {
 //   page-table position jpos of its first page (relative to kv_indptr[0]), and the partial slot
 //   it writes (-1: the segment is the whole pair and writes the final out / lse).
 constexpr int kSegMax = 24;                // segments per workgroup
+constexpr int kStepSegMax = 8;             // segments per workgroup of the fused cascade step at G = 8
 constexpr int kSegInts = 8;
 constexpr int kBalDescInts = 8 + kSegMax * kSegInts;
 constexpr int kRangeMax = 2048;            // pages per workgroup (page ids staged in LDS)

@@ -201,10 +201,13 @@ def test_tree_cascade_without_sharing_falls_back():
     check_lse(l, rl)
 
 
+@pytest.mark.parametrize("Hkv", [8, 4], ids=["G4", "G8"])
 @pytest.mark.parametrize("tree", [False, True], ids=["single-level", "tree"])
-def test_cascade_modes_bitwise_equal(tree):
-    """The fused step (the default at G=4), separate launches on one stream, and the prefix
-    forked onto a second stream: the same arithmetic, so the same bits; against the oracle."""
+def test_cascade_modes_bitwise_equal(tree, Hkv):
+    """The fused step (the default), separate launches on one stream, and the prefix forked onto a
+    second stream: the same arithmetic, so the same bits; against the oracle. At G=8 the fused
+    step's decode role uses its compact layout (the flush in two passes of 4 heads), which
+    computes the same sums in the same order as the plain decode kernel's."""
     import torch
 
     import _gpu
@@ -212,11 +215,11 @@ def test_cascade_modes_bitwise_equal(tree):
     if tree:
         nodes = [((0,), 256), ((0, 1), 512), ((0, 2), 128)]
         seqs = [((0, 1), 40), ((0, 1), 3), ((0, 2), 100), ((0, 2), 16), ((0,), 77)]
-        bt = inputs.make_prefix_tree_batch(nodes, seqs, 32, 8, seed=61)
+        bt = inputs.make_prefix_tree_batch(nodes, seqs, 32, Hkv, seed=61)
     else:
-        bt = inputs.make_shared_prefix_batch(1024, [1] * 70, 32, 8, seed=62)
+        bt = inputs.make_shared_prefix_batch(1024, [1] * 70, 32, Hkv, seed=62)
     db = _gpu.DeviceBatch(bt)
-    print(f"cascade modes: tree={tree}", flush=True)
+    print(f"cascade modes: tree={tree} G={bt.G}", flush=True)
     cp = pdattn.CascadePlan(db.params(), bt.indptr, bt.indices, bt.lens, db.indices, 16, tree)
     ws = pdattn.Workspace()
     got = []
@@ -244,22 +247,22 @@ def test_cascade_modes_bitwise_equal(tree):
     check_lse(l, rl)
 
 
-def test_fused_mode_needs_two_workgroups_per_cu():
-    """At G=8 the fused step's workgroups do not fit two per CU: the plan defaults to separate
-    launches and refuses the fused mode; an unknown mode is refused everywhere."""
+def test_fused_mode_at_g8_and_unknown_mode():
+    """At G=8 the fused step still fits two workgroups per CU (its decode role's compact layout):
+    the plan defaults to it; every mode can be set; an unknown mode is refused."""
     import _gpu
     import pdattn
     bt = inputs.make_shared_prefix_batch(256, [5, 40, 17], 32, 4, seed=63)
     db = _gpu.DeviceBatch(bt)
     cp = pdattn.CascadePlan(db.params(), bt.indptr, bt.indices, bt.lens, db.indices, 16)
     try:
-        assert cp.info().mode == pdattn.CASCADE_SERIAL
-        with pytest.raises(pdattn.PdattnError):
-            cp.set_mode(pdattn.CASCADE_FUSED)
+        assert cp.info().mode == pdattn.CASCADE_FUSED
         with pytest.raises(pdattn.PdattnError):
             cp.set_mode(7)
         cp.set_mode(pdattn.CASCADE_TWO_STREAMS)
         assert cp.info().mode == pdattn.CASCADE_TWO_STREAMS
+        cp.set_mode(pdattn.CASCADE_SERIAL)
+        assert cp.info().mode == pdattn.CASCADE_SERIAL
     finally:
         cp.close()
     o, l, info = _gpu.run_cascade(db, min_prefix=16)
@@ -269,17 +272,19 @@ def test_fused_mode_needs_two_workgroups_per_cu():
     check_lse(l, rl)
 
 
-def test_many_short_sequences_grow_the_suffix_grid():
-    """3500 sequences of 1..16 private tokens behind a 64-token prefix: 7000 (sequence, kv head)
-    pairs need more than one suffix workgroup per CU (at most 24 segments each), so the fused
-    step's prefix blocks start after a grid larger than the CU count."""
+@pytest.mark.parametrize("n,Hq,Hkv", [(3500, 8, 2), (1200, 32, 4)], ids=["G4", "G8"])
+def test_many_short_sequences_grow_the_suffix_grid(n, Hq, Hkv):
+    """n sequences of 1..16 private tokens behind a 64-token prefix: the (sequence, kv head) pairs
+    need more than one suffix workgroup per CU (at most 24 segments each, 8 at G=8, where the
+    fused step's decode role stages q rows for 8), so the fused step's prefix blocks start after a
+    grid larger than the CU count."""
     import _gpu
     import pdattn
     rng = np.random.default_rng(64)
-    suffix = [int(x) for x in rng.integers(1, 17, size=3500)]
-    bt = inputs.make_shared_prefix_batch(64, suffix, 8, 2, seed=64)
+    suffix = [int(x) for x in rng.integers(1, 17, size=n)]
+    bt = inputs.make_shared_prefix_batch(64, suffix, Hq, Hkv, seed=64)
     db = _gpu.DeviceBatch(bt)
-    print("cascade: 3500 short sequences", flush=True)
+    print(f"cascade: {n} short sequences G={bt.G}", flush=True)
     cp = pdattn.CascadePlan(db.params(), bt.indptr, bt.indices, bt.lens, db.indices, 16)
     info = cp.info()
     cp.close()
