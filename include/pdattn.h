@@ -205,9 +205,9 @@ typedef struct pdattn_cascade_plan pdattn_cascade_plan;
 /* How pdattn_cascade_decode runs the prefix pass and the suffix decode (pdattn_cascade_set_mode).
  * FUSED: one launch whose first workgroups decode the suffix and whose others run the prefix
  * items; both roles are 4-wave workgroups small enough for a CU to hold one of each, so every CU
- * streams suffix pages while its matrix core works on the prefix. Default where two of these
- * workgroups fit on a CU (G = 1, 2, 4). SERIAL: the prefix launch, then the suffix decode (the
- * reference's order, cascade_decode 01_decode_attention.cu:703-712); default at G = 8. TWO_STREAMS:
+ * streams suffix pages while its matrix core works on the prefix; the default (at G = 8 the
+ * decode role uses a compact LDS layout so that it fits). SERIAL: the prefix launch, then the
+ * suffix decode (the reference's order, cascade_decode 01_decode_attention.cu:703-712). TWO_STREAMS:
  * the prefix launch forked onto a second stream owned by the plan, joined before the merge. All
  * three compute the same partials with the same kernels' arithmetic: the results are bitwise
  * equal. The merge launch follows in every mode. */
