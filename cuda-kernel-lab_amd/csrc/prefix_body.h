@@ -119,8 +119,31 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
     // same XCD, read the same lines.
     const int sc = tid & 15, sr = tid >> 4;
     pu32x4 kst[KPT], vst[2 * VPT];
+    // A full block (64 keys, starting on a page: kbeg is a multiple of 16) holds pages
+    // 4 kb .. 4 kb + 3 of the chunk: K row i of this thread is slot sr of page 4 kb + i, and V pair
+    // i is slots (2 sr) & 15 and +1 of page 4 kb + (2 sr) / 16 + 2 i. The in-page offsets are
+    // therefore fixed per thread; only the page ids change from block to block.
+    static_assert(KB == 4 * kPage && SR == kPage && KPT == 4 && VPT == 2, "full-block page walk");
+    const uint32_t koff = (uint32_t)((sr * a.Hkv + kvh) * 256 + sc * 16);
+    const uint32_t voff = (uint32_t)((((2 * sr) & 15) * a.Hkv + kvh) * 256 + sc * 16);
+    const uint32_t vstep = (uint32_t)(a.Hkv * 256);   // the next slot of the page
+    const int vpg = (2 * sr) >> 4;
     auto gload = [&](int kb) {
         const int key0 = kbeg + kb * KB;
+        if (key0 + KB <= kend) {
+#pragma unroll
+            for (int i = 0; i < KPT; ++i) {
+                const size_t pid = (uint32_t)sm.pg[4 * kb + i];
+                kst[i] = *reinterpret_cast<const pu32x4*>(a.k + pid * page_bytes + koff);
+            }
+#pragma unroll
+            for (int j = 0; j < VPT; ++j) {
+                const uint8_t* vp = a.v + (size_t)(uint32_t)sm.pg[4 * kb + vpg + 2 * j] * page_bytes + voff;
+                vst[2 * j] = *reinterpret_cast<const pu32x4*>(vp);
+                vst[2 * j + 1] = *reinterpret_cast<const pu32x4*>(vp + vstep);
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int key = min(key0 + sr + SR * i, kend - 1);
