@@ -229,9 +229,12 @@ namespace {
 // (<= kSegMax) segments and kRangeMax pages.
 int build_balanced_plan(const int32_t* indptr, const int32_t* last, int B, int Hq, int Hkv,
                         int force_wg, int chunk_pages, bool merge_all, pdattn_plan* pl,
-                        int seg_cap = kSegMax) {
+                        int seg_cap = 0) {
     int G = 0;
     if (int st = check_heads(Hq, Hkv, &G)) return st;
+    // at G = 8 the decode kernel stages q rows for at most kStepSegMax segments per workgroup
+    const bool wide = G > 4;
+    if (seg_cap <= 0) seg_cap = wide ? kStepSegMax : kSegMax;
     if (B < 0) return fail(PDATTN_ERR_INVALID_ARGUMENT, "B=%d is negative", B);
     if (chunk_pages < 0 || chunk_pages > kRangeMax)
         return fail(PDATTN_ERR_INVALID_ARGUMENT, "chunk_pages=%d outside [0, %d]", chunk_pages, kRangeMax);
@@ -247,13 +250,15 @@ int build_balanced_plan(const int32_t* indptr, const int32_t* last, int B, int H
     pl->nnz = B > 0 ? indptr[B] - indptr[0] : 0;
     pl->U = (int64_t)Hkv * pl->nnz;
 
-    // grid: one workgroup per CU (the kernel's four waves take one SIMD each), never more
+    // grid: one workgroup per CU (the kernel's four waves take one SIMD each; two at G = 8), never more
     // workgroups than page units; a forced size needs no device query
     int64_t W = force_wg;
     if (W <= 0) {
         DeviceFacts f;
         if (int st = device_facts(&f)) return st;
-        W = f.cus;
+        // G = 8 (VALU-limited per page): two workgroups per CU, except for the cascade's suffix,
+        // whose workgroups share the CUs with the prefix pass
+        W = (int64_t)f.cus * (wide && !merge_all ? 2 : 1);
     }
     W = std::max<int64_t>(1, std::min<int64_t>(W, std::max<int64_t>(1, pl->U)));
     W = std::max<int64_t>(W, (pl->U + kRangeMax - 1) / kRangeMax);
@@ -572,9 +577,7 @@ int cascade_plan_create(const pdattn_decode_params* base, const int32_t* h_indpt
             for (int i = h_indptr[b] + start[b]; i < h_indptr[b + 1]; ++i) sidx.push_back(h_indices[i]);
             sind[b + 1] = (int32_t)sidx.size();
         }
-        // at G = 8 the fused step's decode role stages q rows for at most kStepSegMax segments
-        st = build_balanced_plan(sind.data(), last.data(), B, base->Hq, base->Hkv, 0, 0, true, &cp->sk,
-                                 G > 4 ? kStepSegMax : kSegMax);
+        st = build_balanced_plan(sind.data(), last.data(), B, base->Hq, base->Hkv, 0, 0, true, &cp->sk);
         // The prefix work of every node goes into one launch (nodes of different depths write
         // different partial columns, so they are independent). Fused step (default where two of
         // its workgroups fit on a CU): about one prefix workgroup per CU, beside the suffix

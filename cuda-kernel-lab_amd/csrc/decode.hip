@@ -866,10 +866,14 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
     }
 }
 
+// At G = 8 the per-page VALU work is about twice G = 4's and no longer hides under the page's
+// memory time with one wave per SIMD, so the kernel uses the compact LDS layout (61 KB) and the
+// planner gives it two workgroups per CU: the two waves on each SIMD overlap one's arithmetic with
+// the other's loads.
 template <class C>
 __global__ __launch_bounds__(C::NT) void decode_balanced_kernel(BalArgs a) {
-    __shared__ BalShared<C> S;
-    balanced_body<C>(a, S, blockIdx.x);
+    __shared__ BalShared<C, (C::G > 4)> S;
+    balanced_body<C, false, (C::G > 4)>(a, S, blockIdx.x);
 }
 
 // The reference-shaped uniform split on the balanced body (items of equal key ranges, descriptors
