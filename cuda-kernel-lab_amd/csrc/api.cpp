@@ -754,8 +754,11 @@ static int launch_uniform_split(const PartialArgs& a, int G, hipStream_t s) {
     if (int st = device_facts(&f)) return st;
     const int64_t n_items = (int64_t)a.num_chunks * a.B * a.Hkv;
     if (n_items > (int64_t)1 << 30) return fail(PDATTN_ERR_INVALID_ARGUMENT, "too many chunks");
-    int64_t per = (n_items + f.cus - 1) / f.cus;
-    per = std::max<int64_t>(1, std::min<int64_t>({per, (int64_t)kSegMax, kRangeMax / ppi}));
+    // at G = 8 the kernel's compact layout holds kStepSegMax segments, two workgroups per CU
+    const bool wide = G > 4;
+    const int64_t slots = (int64_t)f.cus * (wide ? 2 : 1);
+    int64_t per = (n_items + slots - 1) / slots;
+    per = std::max<int64_t>(1, std::min<int64_t>({per, (int64_t)(wide ? kStepSegMax : kSegMax), kRangeMax / ppi}));
     UniArgs u;
     BalArgs& d = u.d;
     d.q = a.q;

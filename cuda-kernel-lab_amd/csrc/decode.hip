@@ -880,8 +880,8 @@ __global__ __launch_bounds__(C::NT) void decode_balanced_kernel(BalArgs a) {
 // built in the kernel from the device page table).
 template <class C>
 __global__ __launch_bounds__(C::NT) void decode_uniform_kernel(UniArgs u) {
-    __shared__ BalShared<C> S;
-    balanced_body<C, true>(u.d, S, blockIdx.x, &u);
+    __shared__ BalShared<C, (C::G > 4)> S;   // G = 8: compact, two workgroups per CU (as above)
+    balanced_body<C, true, (C::G > 4)>(u.d, S, blockIdx.x, &u);
 }
 
 // The fused cascade step: blocks [0, n_dec) are the suffix decode's workgroups, the rest the

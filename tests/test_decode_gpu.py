@@ -96,6 +96,7 @@ UNIFORM_SHAPES = [
     ("many items per workgroup", "ragged300", 8, 8, 1, 304, 0),         # 2400 items, 10 per workgroup
     ("segment cap per workgroup", "ragged300", 8, 8, 3, 100, 0),        # 7200 items, 24 per workgroup
     ("unaligned start and chunk", [1000, 77, 0, 513], 32, 8, 5, 200, 23),
+    ("G=8, segment cap of the compact layout", "ragged300", 64, 8, 2, 160, 0),   # 4800 items, 8 per workgroup
 ]
 
 
