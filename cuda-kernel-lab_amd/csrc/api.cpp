@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -159,6 +160,72 @@ PartialArgs to_partial_args(const pdattn_decode_params* p) {
     return a;
 }
 
+// ---- schedules resident in device memory ----------------------------------------------------
+// A plan's schedule (segment descriptors and merge list; for a cascade plan also its suffix page
+// table, member lists, prefix items and its -inf lse columns) is copied into a workspace once and
+// read by every run. Each such copy is recorded here as a byte range owned by the plan's id. Every
+// library call that writes device memory (an upload, the partials of a run or of the uniform
+// split, the outputs of any launch) drops the records of other owners that its writes overlap,
+// and a run first checks that its plan's records are all still there: a schedule that another
+// call has overwritten is uploaded again (cascade_decode, which owns its uploads) or reported as
+// PDATTN_ERR_NOT_READY (plan_run, whose caller uploads), never run. The records follow host call
+// order, which is the device order of calls on one stream. Writes the library does not make (the
+// caller's own kernels or copies into a workspace, or freeing it and allocating new memory at the
+// same address) are not seen: after those the caller uploads again.
+struct Resident {
+    uintptr_t lo, hi;
+    uint64_t owner;
+};
+std::mutex g_res_mu;
+std::vector<Resident> g_res;
+std::atomic<uint64_t> g_next_owner{1};
+
+uint64_t new_owner() { return g_next_owner.fetch_add(1); }
+
+void res_drop_locked(uintptr_t lo, uintptr_t hi, uint64_t keep) {
+    g_res.erase(std::remove_if(g_res.begin(), g_res.end(),
+                               [&](const Resident& r) { return r.owner != keep && r.lo < hi && lo < r.hi; }),
+                g_res.end());
+}
+
+// The library is about to write [p, p + n): records of owners other than `keep` there are void.
+void res_written(const void* p, size_t n, uint64_t keep = 0) {
+    if (!p || n == 0) return;
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(p);
+    std::lock_guard<std::mutex> lk(g_res_mu);
+    res_drop_locked(lo, lo + n, keep);
+}
+
+// [p, p + n) now holds part of owner's schedule.
+void res_claim(const void* p, size_t n, uint64_t owner) {
+    if (!p || n == 0) return;
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(p);
+    std::lock_guard<std::mutex> lk(g_res_mu);
+    res_drop_locked(lo, lo + n, 0);   // every record there, the owner's own included
+    g_res.push_back({lo, lo + n, owner});
+}
+
+// Whether [p, p + n) still holds what owner uploaded there.
+bool res_holds(const void* p, size_t n, uint64_t owner) {
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(p);
+    std::lock_guard<std::mutex> lk(g_res_mu);
+    for (const Resident& r : g_res)
+        if (r.owner == owner && r.lo == lo && r.hi == lo + n) return true;
+    return false;
+}
+
+void res_forget(uint64_t owner) {
+    std::lock_guard<std::mutex> lk(g_res_mu);
+    g_res.erase(std::remove_if(g_res.begin(), g_res.end(), [&](const Resident& r) { return r.owner == owner; }),
+                g_res.end());
+}
+
+// out [rows, 128] fp16 and lse [rows] fp32 of a launch.
+void res_written_outputs(const void* out, const void* lse, size_t rows) {
+    res_written(out, rows * kHeadDim * sizeof(_Float16));
+    res_written(lse, rows * sizeof(float));
+}
+
 int ensure_ws(pdattn_workspace* ws, size_t need) {
     if (!ws) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null workspace");
     if (ws->bytes >= need && ws->base) return PDATTN_OK;
@@ -181,7 +248,7 @@ struct pdattn_plan {
     std::vector<int32_t> host_blob;   // desc[W * kBalDescInts] followed by the merge list
     void* pinned = nullptr;           // pinned copy of host_blob for stream-ordered upload
     size_t blob_bytes = 0;
-    const void* uploaded_to = nullptr;
+    uint64_t id = new_owner();        // owner of its uploaded schedules (resident-schedule records)
 };
 
 // One node of a shared-prefix tree: the ns sequences seqs[seq_off ..] all hold the same physical
@@ -208,7 +275,7 @@ struct pdattn_cascade_plan {
     int n_suffix_idx = 0, n_seqs = 0;
     void* pinned = nullptr;
     size_t off_ppo = 0, off_pplse = 0, off_blob = 0, off_sk = 0, ws_bytes = 0;
-    const void* uploaded_to = nullptr;
+    uint64_t id = new_owner();         // owner of its blob and -inf columns in a workspace
     // how the prefix and suffix passes run (pdattn_cascade_set_mode); the second stream of the
     // two-stream mode is created on first use
     int mode = PDATTN_CASCADE_SERIAL;
@@ -363,11 +430,16 @@ int build_balanced_plan(const int32_t* indptr, const int32_t* last, int B, int H
 }
 
 void free_plan_storage(pdattn_plan* pl) {
+    if (pl) res_forget(pl->id);
     if (pl && pl->pinned) {
         (void)hipHostFree(pl->pinned);
         pl->pinned = nullptr;
     }
 }
+
+// Bytes of a plan's schedule in its workspace (descriptors and merge list; the partial slots
+// after them are scratch of each run).
+size_t schedule_bytes(const pdattn_plan* pl) { return pl->off_plse - pl->off_desc; }
 
 int upload_plan(pdattn_plan* pl, void* ws, size_t bytes, hipStream_t s) {
     if (!ws) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null workspace");
@@ -387,7 +459,7 @@ int upload_plan(pdattn_plan* pl, void* ws, size_t bytes, hipStream_t s) {
             PD_HIP(hipMemcpyAsync(base + pl->off_list, static_cast<char*>(pl->pinned) + desc_bytes,
                                   sizeof(int32_t) * 4 * pl->n_entries, hipMemcpyHostToDevice, s));
     }
-    pl->uploaded_to = ws;
+    res_claim(base + pl->off_desc, schedule_bytes(pl), pl->id);
     return PDATTN_OK;
 }
 
@@ -421,8 +493,10 @@ int run_plan(const pdattn_plan* pl, const void* q, const void* k, const void* v,
              void* out, float* lse, void* ws, size_t bytes, hipStream_t s,
              const float* extra_o = nullptr, const float* extra_lse = nullptr, int n_extra = 0,
              hipEvent_t join = nullptr, bool decode = true) {
-    if (ws != pl->uploaded_to)
-        return fail(PDATTN_ERR_NOT_READY, "plan was not uploaded into this workspace");
+    if (!ws || !res_holds(static_cast<char*>(ws) + pl->off_desc, schedule_bytes(pl), pl->id))
+        return fail(PDATTN_ERR_NOT_READY,
+                    "plan's schedule is not in this workspace (never uploaded there, or overwritten "
+                    "since by another upload or launch): upload it again");
     if (bytes < pl->ws_bytes)
         return fail(PDATTN_ERR_WORKSPACE, "workspace holds %zu bytes, plan needs %zu", bytes, pl->ws_bytes);
     if (pl->B == 0) return PDATTN_OK;
@@ -434,6 +508,8 @@ int run_plan(const pdattn_plan* pl, const void* q, const void* k, const void* v,
     char* base = static_cast<char*>(ws);
     float* part_lse = reinterpret_cast<float*>(base + pl->off_plse);
     float* part_o = reinterpret_cast<float*>(base + pl->off_po);
+    res_written(part_lse, pl->ws_bytes - pl->off_plse, pl->id);
+    res_written_outputs(out, lse, (size_t)pl->B * pl->Hq);
     if (pl->U > 0 && decode)
         PD_HIP(launch_decode_balanced(bal_args(pl, q, k, v, indices, sm_scale, out, lse, base), pl->G, s));
     if (join) PD_HIP(hipStreamWaitEvent(s, join, 0));
@@ -686,6 +762,7 @@ int pdattn_workspace_reserve(pdattn_workspace* ws, size_t bytes) {
         return fail(PDATTN_ERR_WORKSPACE, "caller-provided workspace holds %zu bytes, %zu needed", ws->bytes, bytes);
     if (ws->base) {
         PD_HIP(hipDeviceSynchronize());
+        res_written(ws->base, ws->bytes);   // freed: what was uploaded there is gone
         PD_HIP(hipFree(ws->base));
         ws->base = nullptr;
         ws->bytes = 0;
@@ -702,11 +779,26 @@ void pdattn_workspace_release(pdattn_workspace* ws) {
     if (!ws) return;
     if (ws->base && ws->owned) {
         (void)hipDeviceSynchronize();
+        res_written(ws->base, ws->bytes);
         (void)hipFree(ws->base);
     }
     ws->base = nullptr;
     ws->bytes = 0;
     ws->owned = 0;
+}
+
+int pdattn_check_page_table(const int32_t* h_indptr, const int32_t* h_indices, const int32_t* h_last,
+                            int B, int64_t num_pages) {
+    if (B < 0 || num_pages < 0) return fail(PDATTN_ERR_INVALID_ARGUMENT, "B=%d num_pages=%lld", B, (long long)num_pages);
+    if (!h_indptr) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null kv_indptr");
+    if (int st = check_host_table(h_indptr, h_last, B)) return st;
+    if (h_indptr[B] > h_indptr[0] && !h_indices) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null kv_indices");
+    for (int b = 0; b < B; ++b)
+        for (int j = h_indptr[b]; j < h_indptr[b + 1]; ++j)
+            if (h_indices[j] < 0 || h_indices[j] >= num_pages)
+                return fail(PDATTN_ERR_PAGE_TABLE, "kv_indices[%d] = %d (page %d of sequence %d) outside [0, %lld)",
+                            j, h_indices[j], j - h_indptr[b], b, (long long)num_pages);
+    return PDATTN_OK;
 }
 
 int pdattn_plan_chunks(int G, int variant, int B, int Hkv, int max_len, int force_chunks,
@@ -793,6 +885,9 @@ int pdattn_decode_partial(const pdattn_decode_params* p, int G, int variant, voi
     if (int st = check_decode_params(p, G)) return st;
     if (p->B == 0) return PDATTN_OK;
     if (!p->part_o || !p->part_lse) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null part_o / part_lse");
+    const size_t slots = (size_t)p->B * p->Hq * p->part_stride;
+    res_written(p->part_o, slots * kHeadDim * sizeof(float));
+    res_written(p->part_lse, slots * sizeof(float));
     return launch_uniform_split(to_partial_args(p), G, static_cast<hipStream_t>(stream));
 }
 
@@ -801,6 +896,7 @@ int pdattn_merge_states(const float* part_o, const float* part_lse, void* out, f
     if (rows < 0 || num_chunks < 1) return fail(PDATTN_ERR_INVALID_ARGUMENT, "rows=%d num_chunks=%d", rows, num_chunks);
     if (rows == 0) return PDATTN_OK;
     if (!part_o || !part_lse || !out || !lse_out) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null pointer");
+    res_written_outputs(out, lse_out, (size_t)rows);
     PD_HIP(launch_merge_states(part_o, part_lse, static_cast<_Float16*>(out), lse_out, rows, num_chunks,
                                static_cast<hipStream_t>(stream)));
     return PDATTN_OK;
@@ -836,6 +932,8 @@ int pdattn_decode_attention(const pdattn_decode_params* p, int G, int variant, v
     if (int st = ensure_ws(ws, need)) return st;
     pdattn_decode_params q = *p;
     if (int st = pdattn_workspace_partials(ws, p->B, p->Hq, p->part_stride, &q.part_o, &q.part_lse)) return st;
+    res_written(ws->base, need);   // the partials: any schedule uploaded there is overwritten
+    res_written_outputs(out, lse, (size_t)p->B * p->Hq);
     hipStream_t s = static_cast<hipStream_t>(stream);
     PartialArgs a = to_partial_args(&q);
     if (p->num_chunks == 1) {
@@ -961,6 +1059,9 @@ int pdattn_cascade_prefix(const pdattn_prefix_params* p, void* stream) {
     a.ns = p->B;
     a.col0 = 0;
     a.scale_log2 = p->sm_scale * 1.4426950408889634f;
+    const size_t slots = (size_t)p->B * p->Hq * p->part_stride;
+    res_written(p->part_o, slots * kHeadDim * sizeof(float));
+    res_written(p->part_lse, slots * sizeof(float));
     const int rows = prefix_rows_per_workgroup();
     const int qtiles = (p->B * G + rows - 1) / rows;
     PD_HIP(launch_cascade_prefix(a, G, qtiles, static_cast<hipStream_t>(stream)));
@@ -1006,22 +1107,30 @@ int pdattn_cascade_decode(pdattn_cascade_plan* cp, void* out, float* lse, pdattn
     const pdattn_decode_params& p = cp->base;
     float* ppo = reinterpret_cast<float*>(base + cp->off_ppo);
     float* pplse = reinterpret_cast<float*>(base + cp->off_pplse);
-    if (cp->uploaded_to != ws->base) {
+    const size_t n_lse = (size_t)p.B * p.Hq * cp->n_extra;
+    const size_t blob_bytes = cp->blob.size() * sizeof(int32_t);
+    const bool resident =
+        res_holds(base + cp->off_sk + cp->sk.off_desc, schedule_bytes(&cp->sk), cp->sk.id) &&
+        (!cp->use || (res_holds(base + cp->off_blob, blob_bytes, cp->id) &&
+                      (n_lse == 0 || res_holds(pplse, n_lse * sizeof(float), cp->id))));
+    if (!resident) {
+        // first call with this workspace, or another call has written over the plan's part of it
         if (cp->use && !cp->pinned) {
             hipError_t e = hipHostMalloc(&cp->pinned, cp->blob.size() * sizeof(int32_t), hipHostMallocDefault);
             if (e != hipSuccess) return hip_fail(e, "hipHostMalloc(cascade plan)");
             std::memcpy(cp->pinned, cp->blob.data(), cp->blob.size() * sizeof(int32_t));
         }
         if (cp->use) {
-            PD_HIP(hipMemcpyAsync(base + cp->off_blob, cp->pinned, cp->blob.size() * sizeof(int32_t),
-                                  hipMemcpyHostToDevice, s));
+            PD_HIP(hipMemcpyAsync(base + cp->off_blob, cp->pinned, blob_bytes, hipMemcpyHostToDevice, s));
+            res_claim(base + cp->off_blob, blob_bytes, cp->id);
             // partial columns no node writes for a row stay empty (lse = -inf) for good
-            const size_t n_lse = (size_t)p.B * p.Hq * cp->n_extra;
             PD_HIP(launch_fill_i32(reinterpret_cast<int32_t*>(pplse), (int32_t)0xff800000u, n_lse, s));
+            res_claim(pplse, n_lse * sizeof(float), cp->id);
         }
         if (int st = upload_plan(&cp->sk, base + cp->off_sk, cp->sk.ws_bytes, s)) return st;
-        cp->uploaded_to = ws->base;
     }
+    // the prefix pass writes the node columns of the partials (the -inf columns stay as filled)
+    res_written(ppo, cp->off_pplse - cp->off_ppo, cp->id);
     if (!cp->use)
         return run_plan(&cp->sk, p.q, p.k_cache, p.v_cache, p.kv_indptr, p.kv_indices,
                         p.kv_last_page_len, p.sm_scale, out, lse, base + cp->off_sk, cp->sk.ws_bytes, s);
@@ -1052,7 +1161,7 @@ int pdattn_cascade_decode(pdattn_cascade_plan* cp, void* out, float* lse, pdattn
     char* skb = base + cp->off_sk;
     if (cp->mode == PDATTN_CASCADE_FUSED) {
         // one launch: the suffix decode's workgroups, then the prefix workgroups beside them
-        if (cp->sk.ws_bytes > 0 && skb != cp->sk.uploaded_to)
+        if (!res_holds(skb + cp->sk.off_desc, schedule_bytes(&cp->sk), cp->sk.id))
             return fail(PDATTN_ERR_NOT_READY, "suffix plan was not uploaded into this workspace");
         StepArgs sa;
         sa.d = bal_args(&cp->sk, p.q, p.k_cache, p.v_cache, sidx, p.sm_scale, out, lse, skb);
@@ -1107,6 +1216,7 @@ void pdattn_cascade_plan_destroy(pdattn_cascade_plan* cp) {
     if (cp->ev_join) (void)hipEventDestroy(cp->ev_join);
     if (cp->aux) (void)hipStreamDestroy(cp->aux);
     free_plan_storage(&cp->sk);
+    res_forget(cp->id);
     if (cp->pinned) (void)hipHostFree(cp->pinned);
     delete cp;
 }

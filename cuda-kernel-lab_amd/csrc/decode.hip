@@ -177,14 +177,29 @@ __device__ __forceinline__ void load_page_rsrc(PageRegs<C>& pr, __amdgpu_buffer_
         }
 }
 
-// One page: scores, online-softmax update, PV accumulation. tok_r is the token index of this
-// lane's row in row group 0; keys outside [tb, te) are masked.
+// One page: scores, online-softmax update, PV accumulation. tok0 is the (wave-uniform) token
+// index of the page's first slot, and this lane's row of row group i is slot r + i * RPI; keys
+// outside [tb, te) are masked. A masked key gets weight 0, and on a page that holds masked keys
+// (the first or last page of a range) their V rows are zeroed as well, so that slots the cache
+// never filled (NaN or Inf bit patterns in unused slots of a last page) cannot reach the output
+// through 0 * v.
 template <class C>
-__device__ __forceinline__ void page_step(WaveState<C>& st, const PageRegs<C>& pr,
-                                          const f16x2 (&qv)[C::G][C::PPL][4], int tok_r,
+__device__ __forceinline__ void page_step(WaveState<C>& st, PageRegs<C>& pr,
+                                          const f16x2 (&qv)[C::G][C::PPL][4], int tok0, int r,
                                           int tb, int te, float scale2) {
     using g = C;
     constexpr int G = C::G;
+    const int tok_r = tok0 + r;
+    if (tok0 < tb || tok0 + kPage > te) {   // wave-uniform: an edge page
+#pragma unroll
+        for (int i = 0; i < g::RG; ++i) {
+            const int tok = tok_r + i * g::RPI;
+            if (tok < tb || tok >= te) {
+#pragma unroll
+                for (int kk = 0; kk < g::PPL; ++kk) pr.v[i][kk] = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    }
     float x[g::RG][G];
 #pragma unroll
     for (int i = 0; i < g::RG; ++i) {
@@ -317,7 +332,7 @@ __device__ __forceinline__ void process_range(Smem<C::G, C::NW>& sm, const _Floa
                 for (int u = 0; u < NBUF; ++u) {
                     if (it + u >= cnt) break;
                     issue(buf[(u + NBUF - 1) % NBUF], pidv, it + u + NBUF - 1, cnt);
-                    page_step<C>(st, buf[u], qv, tok_base + (pfirst + wave + NW * (base + it + u)) * kPage + r,
+                    page_step<C>(st, buf[u], qv, tok_base + (pfirst + wave + NW * (base + it + u)) * kPage, r,
                                  t0, t1, scale2);
                 }
             }
@@ -855,7 +870,7 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
             for (int u = 0; u < NBUF; ++u) {
                 issue(buf[(u + NBUF - 1) % NBUF]);
                 if (blk + u < cnt)
-                    page_step<C>(st, buf[u], qv, tbase + (wave + NW * (blk + u)) * kPage + r, t0, t1,
+                    page_step<C>(st, buf[u], qv, tbase + (wave + NW * (blk + u)) * kPage, r, t0, t1,
                                  a.scale_log2);
             }
         }

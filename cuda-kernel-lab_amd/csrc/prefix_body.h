@@ -201,6 +201,7 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
         for (int ks = 0; ks < 4; ++ks)
             if (qrow[tq] < 0) qb[tq][ks] = pf16x8{};
 
+    const bool neg = a.scale_log2 < 0.f;   // the extremum that scales to the maximum is the minimum
     pf32x4 acc[NT][8];
     float m_run[NT], l_run[NT];
 #pragma unroll
@@ -236,30 +237,43 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
             }
         }
 
-        // Online softmax (base 2) per query. The scores stay unscaled: the maximum is taken on
-        // them and scaled once (the scale is positive, so this is the maximum of the scaled
-        // scores), and each weight is exp2(fma(s, scale, -m)). Only a block that runs past the
-        // chunk's end masks its keys (to -inf, weight 0).
+        // Online softmax (base 2) per query. The scores stay unscaled: the maximum of the scaled
+        // scores is the scale times the maximum of the unscaled ones (the minimum for a negative
+        // scale), and each weight is exp2(fma(s, scale, -m)). Only a block that runs past the
+        // chunk's end holds masked keys: their scores are set to the value the extremum ignores
+        // (-inf, or +inf for a negative scale) and their weights to 0 below.
         const int kbase = kbeg + kb * KB + 4 * lg;
-        if (kbeg + (kb + 1) * KB > kend) {
+        const bool edge = kbeg + (kb + 1) * KB > kend;   // uniform over the workgroup
+        if (edge) {
+            const float ignore = neg ? INFINITY : -INFINITY;
 #pragma unroll
             for (int tq = 0; tq < NT; ++tq)
 #pragma unroll
                 for (int tk = 0; tk < 4; ++tk)
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
-                        if (kbase + 16 * tk + j >= kend) s[tq][tk][j] = -INFINITY;
+                        if (kbase + 16 * tk + j >= kend) s[tq][tk][j] = ignore;
         }
         float mn[NT];
         bool grow = false;
 #pragma unroll
         for (int tq = 0; tq < NT; ++tq) {
-            float mx = -INFINITY;
+            float mx;
+            if (!neg) {
+                mx = -INFINITY;
 #pragma unroll
-            for (int tk = 0; tk < 4; ++tk)
+                for (int tk = 0; tk < 4; ++tk)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) mx = fmaxf(mx, s[tq][tk][j]);
-            mx = col4_reduce<true>(mx);
+                    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, s[tq][tk][j]);
+                mx = col4_reduce<true>(mx);
+            } else {
+                mx = INFINITY;
+#pragma unroll
+                for (int tk = 0; tk < 4; ++tk)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) mx = fminf(mx, s[tq][tk][j]);
+                mx = -col4_reduce<true>(-mx);
+            }
             mn[tq] = fmaxf(m_run[tq], mx * a.scale_log2);
             grow |= mn[tq] > m_run[tq];
         }
@@ -277,13 +291,24 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
 #pragma unroll
         for (int tq = 0; tq < NT; ++tq) {
             const float ms = (m_run[tq] == -INFINITY) ? 0.f : m_run[tq];
+            float pw[4][4];
+#pragma unroll
+            for (int tk = 0; tk < 4; ++tk)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) pw[tk][j] = __builtin_amdgcn_exp2f(fmaf(s[tq][tk][j], a.scale_log2, -ms));
+            if (edge) {   // masked keys weigh 0 whatever the scale (0 * inf would not)
+#pragma unroll
+                for (int tk = 0; tk < 4; ++tk)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (kbase + 16 * tk + j >= kend) pw[tk][j] = 0.f;
+            }
 #pragma unroll
             for (int tk = 0; tk < 4; ++tk)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const float p = __builtin_amdgcn_exp2f(fmaf(s[tq][tk][j], a.scale_log2, -ms));
-                    l_run[tq] += p;   // fp32 weights for the denominator (exact lse); PV uses
-                    pb[tq][tk >> 1][(tk & 1) * 4 + j] = (_Float16)p;   // them rounded to nearest
+                    l_run[tq] += pw[tk][j];   // fp32 weights for the denominator (exact lse); PV
+                    pb[tq][tk >> 1][(tk & 1) * 4 + j] = (_Float16)pw[tk][j];   // uses them rounded to nearest
                 }
         }
 

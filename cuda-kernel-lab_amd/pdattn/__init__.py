@@ -35,6 +35,7 @@ STATUS = {
 EXPORTS = [
     "pdattn_strerror", "pdattn_last_error",
     "pdattn_workspace_reserve", "pdattn_workspace_release",
+    "pdattn_check_page_table",
     "pdattn_plan_chunks", "pdattn_decode_partial", "pdattn_merge_states",
     "pdattn_decode_workspace_size", "pdattn_workspace_partials", "pdattn_decode_attention",
     "pdattn_plan_create", "pdattn_plan_get_info", "pdattn_plan_workspace_size",
@@ -133,6 +134,7 @@ def lib():
         "pdattn_last_error": ([], ctypes.c_char_p),
         "pdattn_workspace_reserve": ([ctypes.POINTER(Workspace), S], I),
         "pdattn_workspace_release": ([ctypes.POINTER(Workspace)], None),
+        "pdattn_check_page_table": ([P, P, P, I, ctypes.c_int64], I),
         "pdattn_plan_chunks": ([I, I, I, I, I, I, ctypes.POINTER(I), ctypes.POINTER(I)], I),
         "pdattn_decode_partial": ([ctypes.POINTER(DecodeParams), I, I, P], I),
         "pdattn_merge_states": ([P, P, P, P, I, I, P], I),
@@ -199,6 +201,17 @@ def host_i32(a):
     if arr.size == 0:
         arr = np.zeros(1, np.int32)
     return arr, arr.ctypes.data_as(ctypes.c_void_p)
+
+
+def check_page_table(kv_indptr, kv_indices, kv_last_page_len, num_pages: int):
+    """pdattn_check_page_table on host copies of a page table: raises PdattnError
+    (PDATTN_ERR_PAGE_TABLE) for a decreasing indptr, a page id outside [0, num_pages) or a last
+    page length outside [1, 16]."""
+    ip, ipp = host_i32(kv_indptr)
+    ix, ixp = host_i32(kv_indices)
+    la, lap = host_i32(kv_last_page_len)
+    B = len(ip) - 1 if len(kv_indptr) > 0 else 0
+    _check(lib().pdattn_check_page_table(ipp, ixp, lap, B, int(num_pages)), "pdattn_check_page_table")
 
 
 # ---- reference-shaped split-KV path ------------------------------------------------------------

@@ -40,10 +40,11 @@ typedef enum pdattn_status {
     PDATTN_OK = 0,
     PDATTN_ERR_INVALID_ARGUMENT = 1, /* null pointer, negative size, inconsistent chunking      */
     PDATTN_ERR_UNSUPPORTED = 2,      /* G not in {1,2,4,8}, Hq % Hkv != 0                        */
-    PDATTN_ERR_PAGE_TABLE = 3,       /* indptr not monotone, last_page_len outside [1,16]        */
+    PDATTN_ERR_PAGE_TABLE = 3,       /* indptr not monotone, last_page_len outside [1,16], page
+                                        id outside the cache (pdattn_check_page_table)            */
     PDATTN_ERR_WORKSPACE = 4,        /* caller-provided workspace smaller than required          */
     PDATTN_ERR_HIP = 5,              /* a HIP runtime call failed (detail in pdattn_last_error)  */
-    PDATTN_ERR_NOT_READY = 6         /* plan not uploaded into this workspace                    */
+    PDATTN_ERR_NOT_READY = 6         /* plan's schedule not (or no longer) in this workspace     */
 } pdattn_status;
 
 /* Name of a status code. */
@@ -88,6 +89,16 @@ typedef struct pdattn_workspace {
 int pdattn_workspace_reserve(pdattn_workspace* ws, size_t bytes);
 /* Free an owned workspace and zero the struct (the reference's cudaFree at 01:893). */
 void pdattn_workspace_release(pdattn_workspace* ws);
+
+/* Host-side check of a page table against a cache of num_pages pages: kv_indptr [B+1] starts at
+ * 0 or more and never decreases, every kv_indices entry in [kv_indptr[0], kv_indptr[B]) lies in
+ * [0, num_pages), and every non-empty sequence's kv_last_page_len lies in [1, 16]. Returns
+ * PDATTN_OK, PDATTN_ERR_PAGE_TABLE (the first offending position is in pdattn_last_error) or
+ * PDATTN_ERR_INVALID_ARGUMENT. The decode kernels read page ids as given, with no bounds check on
+ * the device (the launch API carries no cache size): a caller that does not build the table
+ * itself checks it here first. No counterpart in the reference, which validates no input. */
+int pdattn_check_page_table(const int32_t* h_kv_indptr, const int32_t* h_kv_indices,
+                            const int32_t* h_kv_last_page_len, int B, int64_t num_pages);
 
 /* ---- reference-shaped split-KV path (uniform chunks) ------------------------------------- */
 
@@ -162,7 +173,12 @@ size_t pdattn_plan_workspace_size(const pdattn_plan* plan);
  * For inspection and tests; `count` must be at least info.schedule_ints. */
 int pdattn_plan_get_schedule(const pdattn_plan* plan, int32_t* out, size_t count);
 /* Stream-ordered copy of the plan's schedule into `workspace`. Must precede pdattn_plan_run with
- * that workspace; the plan may then be run any number of times. */
+ * that workspace; the plan may then be run any number of times, until another library call writes
+ * over the schedule's bytes (another plan's upload or run, or decode_attention's partials in the
+ * same memory): pdattn_plan_run then returns PDATTN_ERR_NOT_READY instead of running on what it
+ * finds there, and the plan is uploaded again. Writes the library does not make (the caller's own
+ * kernels or copies into the workspace, or its memory freed and allocated again at the same
+ * address) are not seen: after those the caller uploads again. */
 int pdattn_plan_upload(pdattn_plan* plan, void* workspace, size_t bytes, void* stream);
 /* Attention for every (sequence, q head) of the planned batch: the decode launch and, when the
  * plan has split pairs or empty sequences, the merge launch. The device page table must hold the
@@ -251,7 +267,8 @@ int pdattn_cascade_tree_plan_create(const pdattn_decode_params* base, const int3
 int pdattn_cascade_plan_get_info(const pdattn_cascade_plan* plan, pdattn_cascade_info* info);
 /* Prefix pass, suffix decode and merge on `stream` (cascade_decode, 01_decode_attention.cu:703-712),
  * as the plan's mode says. The first call with a given workspace uploads the plan's schedule into
- * it (stream-ordered). */
+ * it (stream-ordered), and so does any later call after another library call (another plan's
+ * decode, decode_attention) has written over it: plans may share one pdattn_workspace. */
 int pdattn_cascade_decode(pdattn_cascade_plan* plan, void* out, float* lse, pdattn_workspace* ws,
                           void* stream);
 /* Choose how the prefix pass and the suffix decode run (PDATTN_CASCADE_*): both overlap (FUSED,

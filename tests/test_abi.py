@@ -145,3 +145,26 @@ def test_plan_run_requires_upload():
     with pytest.raises(pdattn.PdattnError) as e:
         plan.run(1 << 20, 1 << 20, 1 << 20, 1 << 20, 1 << 20, 1 << 20, 1 << 20, 1 << 20, 1 << 20, 1 << 30)
     assert e.value.status == 6
+
+
+def test_check_page_table():
+    """pdattn_check_page_table: each malformed table is rejected with PDATTN_ERR_PAGE_TABLE."""
+    good = ([0, 2, 2, 5], [4, 0, 3, 1, 2], [7, 0, 16])
+    pdattn.check_page_table(*good, num_pages=5)
+    pdattn.check_page_table([0], [], [], num_pages=0)   # no sequences
+    bad = [
+        (([0, 2, 1, 5], [4, 0, 3, 1, 2], [7, 0, 16]), 5, "indptr decreases"),
+        (([-1, 2, 2, 5], [4, 0, 3, 1, 2, 0], [7, 0, 16]), 5, "negative indptr"),
+        (([0, 2, 2, 5], [4, 0, 3, 5, 2], [7, 0, 16]), 5, "page id == num_pages"),
+        (([0, 2, 2, 5], [4, -1, 3, 1, 2], [7, 0, 16]), 5, "negative page id"),
+        (([0, 2, 2, 5], [4, 0, 3, 1, 2], [0, 0, 16]), 5, "last page length 0"),
+        (([0, 2, 2, 5], [4, 0, 3, 1, 2], [7, 0, 17]), 5, "last page length 17"),
+        (([0, 2, 2, 5], [4, 0, 3, 1, 2], [7, 0, 16]), 4, "page id beyond a smaller cache"),
+    ]
+    for (ip, ix, la), n, what in bad:
+        with pytest.raises(pdattn.PdattnError) as e:
+            pdattn.check_page_table(ip, ix, la, num_pages=n)
+        assert e.value.status == 3, what
+    with pytest.raises(pdattn.PdattnError) as e:
+        pdattn.check_page_table(*good, num_pages=-1)
+    assert e.value.status == 1
