@@ -919,8 +919,12 @@ int pdattn_workspace_partials(const pdattn_workspace* ws, int B, int Hq, int par
     return PDATTN_OK;
 }
 
-int pdattn_decode_attention(const pdattn_decode_params* p, int G, int variant, void* out,
-                            float* lse, pdattn_workspace* ws, void* stream) {
+}  // extern "C"
+
+namespace pdattn {
+
+int decode_attention_check(const pdattn_decode_params* p, int G, int variant, const void* out,
+                           const float* lse) {
     if (variant < 0 || variant > 3) return fail(PDATTN_ERR_INVALID_ARGUMENT, "variant %d not in 0..3", variant);
     if (int st = check_decode_params(p, G)) return st;
     if (p->B == 0) return PDATTN_OK;
@@ -928,13 +932,15 @@ int pdattn_decode_attention(const pdattn_decode_params* p, int G, int variant, v
     // the merge reads part_stride slots per row: every one of them must be written by this call
     if (p->chunk_base != 0 || p->part_stride != p->num_chunks)
         return fail(PDATTN_ERR_INVALID_ARGUMENT, "decode_attention needs chunk_base = 0 and part_stride = num_chunks");
-    const size_t need = pdattn_decode_workspace_size(p->B, p->Hq, p->part_stride);
-    if (int st = ensure_ws(ws, need)) return st;
-    pdattn_decode_params q = *p;
-    if (int st = pdattn_workspace_partials(ws, p->B, p->Hq, p->part_stride, &q.part_o, &q.part_lse)) return st;
-    res_written(ws->base, need);   // the partials: any schedule uploaded there is overwritten
+    return PDATTN_OK;
+}
+
+int decode_attention_launch(const pdattn_decode_params* p, int G, void* out, float* lse, float* part_o,
+                            float* part_lse, hipStream_t s) {
     res_written_outputs(out, lse, (size_t)p->B * p->Hq);
-    hipStream_t s = static_cast<hipStream_t>(stream);
+    pdattn_decode_params q = *p;
+    q.part_o = part_o;
+    q.part_lse = part_lse;
     PartialArgs a = to_partial_args(&q);
     if (p->num_chunks == 1) {
         // one chunk per sequence: the partial kernel writes the result (merge_states of a single
@@ -944,9 +950,27 @@ int pdattn_decode_attention(const pdattn_decode_params* p, int G, int variant, v
         return launch_uniform_split(a, G, s);
     }
     if (int st = launch_uniform_split(a, G, s)) return st;
-    PD_HIP(launch_merge_states(q.part_o, q.part_lse, static_cast<_Float16*>(out), lse, p->B * p->Hq,
+    PD_HIP(launch_merge_states(part_o, part_lse, static_cast<_Float16*>(out), lse, p->B * p->Hq,
                                p->part_stride, s));
     return PDATTN_OK;
+}
+
+int report_error(int status, const char* what) { return fail(status, "%s", what); }
+
+}  // namespace pdattn
+
+extern "C" {
+
+int pdattn_decode_attention(const pdattn_decode_params* p, int G, int variant, void* out,
+                            float* lse, pdattn_workspace* ws, void* stream) {
+    if (int st = decode_attention_check(p, G, variant, out, lse)) return st;
+    if (p->B == 0) return PDATTN_OK;
+    const size_t need = pdattn_decode_workspace_size(p->B, p->Hq, p->part_stride);
+    if (int st = ensure_ws(ws, need)) return st;
+    float *part_o = nullptr, *part_lse = nullptr;
+    if (int st = pdattn_workspace_partials(ws, p->B, p->Hq, p->part_stride, &part_o, &part_lse)) return st;
+    res_written(ws->base, need);   // the partials: any schedule uploaded there is overwritten
+    return decode_attention_launch(p, G, out, lse, part_o, part_lse, static_cast<hipStream_t>(stream));
 }
 
 int pdattn_plan_create(const int32_t* h_kv_indptr, const int32_t* h_kv_last_page_len, int B,

@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "../../include/pdattn.h"
+
 namespace pdattn {
 
 constexpr int kHeadDim = 128;
@@ -146,6 +148,16 @@ hipError_t launch_cascade_step(const StepArgs& a, int G, hipStream_t s);
 hipError_t launch_append_kv(const AppendArgs& a, int cus, hipStream_t s);
 hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, int grid, hipStream_t s);
 hipError_t launch_flush(void* buf, size_t bytes, int grid, hipStream_t s);
+
+// The uniform split behind decode_attention (api.cpp), shared by the no-allocation entry point:
+// argument checks (a status; PDATTN_OK for B = 0 too), and the launches with the partial states
+// at part_o / part_lse (B * Hq * part_stride slots; unused when num_chunks = 1).
+int decode_attention_check(const pdattn_decode_params* p, int G, int variant, const void* out,
+                           const float* lse);
+int decode_attention_launch(const pdattn_decode_params* p, int G, void* out, float* lse, float* part_o,
+                            float* part_lse, hipStream_t s);
+// Sets the message pdattn_last_error returns and passes the status through.
+int report_error(int status, const char* what);
 
 // Occupancy (workgroups per CU) of the kernels, queried from the runtime.
 int occupancy_decode_partial(int G);

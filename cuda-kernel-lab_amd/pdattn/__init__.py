@@ -38,6 +38,7 @@ EXPORTS = [
     "pdattn_check_page_table",
     "pdattn_plan_chunks", "pdattn_decode_partial", "pdattn_merge_states",
     "pdattn_decode_workspace_size", "pdattn_workspace_partials", "pdattn_decode_attention",
+    "pdattn_decode_attention_noalloc",
     "pdattn_plan_create", "pdattn_plan_get_info", "pdattn_plan_workspace_size",
     "pdattn_plan_get_schedule", "pdattn_plan_upload", "pdattn_plan_run", "pdattn_plan_destroy",
     "pdattn_shared_prefix_pages", "pdattn_cascade_prefix",
@@ -143,6 +144,7 @@ def lib():
                                        ctypes.POINTER(P), ctypes.POINTER(P)], I),
         "pdattn_decode_attention": ([ctypes.POINTER(DecodeParams), I, I, P, P,
                                      ctypes.POINTER(Workspace), P], I),
+        "pdattn_decode_attention_noalloc": ([ctypes.POINTER(DecodeParams), I, I, P, P, P], I),
         "pdattn_plan_create": ([P, P, I, I, I, I, I, ctypes.POINTER(P)], I),
         "pdattn_plan_get_info": ([P, ctypes.POINTER(PlanInfo)], I),
         "pdattn_plan_get_schedule": ([P, P, S], I),
@@ -262,6 +264,16 @@ def workspace_partials(ws: Workspace, B: int, Hq: int, part_stride: int):
 def decode_attention(p: DecodeParams, G: int, out, lse, ws: Workspace, stream=None, variant: int = 0):
     _check(lib().pdattn_decode_attention(ctypes.byref(p), G, variant, ptr(out), ptr(lse),
                                          ctypes.byref(ws), stream_ptr(stream)), "pdattn_decode_attention")
+
+
+NOALLOC_SCRATCH_BYTES = 16 << 20   # PDATTN_NOALLOC_SCRATCH_BYTES
+
+
+def decode_attention_noalloc(p: DecodeParams, G: int, out, lse, stream=None, variant: int = 0):
+    """pdattn_decode_attention_noalloc: decode_attention with the partial states in the library's
+    own device array (no allocation, no workspace)."""
+    _check(lib().pdattn_decode_attention_noalloc(ctypes.byref(p), G, variant, ptr(out), ptr(lse),
+                                                 stream_ptr(stream)), "pdattn_decode_attention_noalloc")
 
 
 def workspace_reserve(ws: Workspace, nbytes: int):

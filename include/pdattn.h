@@ -132,6 +132,21 @@ int pdattn_workspace_partials(const pdattn_workspace* ws, int B, int Hq, int par
 int pdattn_decode_attention(const pdattn_decode_params* p, int G, int variant, void* out,
                             float* lse, pdattn_workspace* ws, void* stream);
 
+/* Bytes of the device array pdattn_decode_attention_noalloc keeps its partial states in (16 MiB
+ * on every GPU the library runs on, held until the process ends). */
+#define PDATTN_NOALLOC_SCRATCH_BYTES (16u << 20)
+
+/* pdattn_decode_attention without allocating: the partial states go to the library's own device
+ * array (PDATTN_NOALLOC_SCRATCH_BYTES per GPU) instead of a workspace, so the call makes no
+ * hipMalloc / hipFree and needs no workspace argument. No counterpart in the reference; it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops that
+ * forbid hipMalloc). The partial states must fit the array: pdattn_decode_workspace_size(B, Hq,
+ * part_stride) <= PDATTN_NOALLOC_SCRATCH_BYTES when num_chunks > 1 (one chunk needs none), else
+ * PDATTN_ERR_WORKSPACE. Every call on one GPU uses the same array: calls that overlap in time on
+ * one GPU (two streams, two host threads) race, and the caller serializes them. */
+int pdattn_decode_attention_noalloc(const pdattn_decode_params* p, int G, int variant, void* out,
+                                    float* lse, void* stream);
+
 /* ---- balanced path (plan / run) ---------------------------------------------------------- */
 /* The MI355X path for decode_attention. The planner works on the host, from the host copy of the
  * page table, the way FlashInfer's plan() does. It cuts every (sequence, kv head) pair into chunks

@@ -168,3 +168,18 @@ def test_check_page_table():
     with pytest.raises(pdattn.PdattnError) as e:
         pdattn.check_page_table(*good, num_pages=-1)
     assert e.value.status == 1
+
+
+def test_noalloc_rejects_partials_beyond_its_array():
+    """pdattn_decode_attention_noalloc refuses, before any GPU call, a request whose partial states
+    exceed PDATTN_NOALLOC_SCRATCH_BYTES; a single chunk needs no partial states."""
+    B, Hq, chunks = 64, 32, 256   # 64 * 32 * 256 slots * 516 B = 270 MB
+    assert pdattn.decode_workspace_size(B, Hq, chunks) > pdattn.NOALLOC_SCRATCH_BYTES
+    p = _params(B=B, Hq=Hq, Hkv=8, num_chunks=chunks, chunk_tokens=16)
+    with pytest.raises(pdattn.PdattnError) as e:
+        pdattn.decode_attention_noalloc(p, 4, 1 << 20, 1 << 20)
+    assert e.value.status == 4
+    p = _params(num_chunks=2, chunk_base=1, part_stride=3)
+    with pytest.raises(pdattn.PdattnError) as e:
+        pdattn.decode_attention_noalloc(p, 4, 1 << 20, 1 << 20)
+    assert e.value.status == 1
