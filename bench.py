@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--only", default="", choices=["", "32k", "64x1k", "cascade", "cascade8", "prefix", "append",
-                                                   "graph", "tree"],
+                                                   "graph", "tree", "legs"],
                     help="run one workload only (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only torch copies of COPY_BYTES (known-size traffic for counter runs)")
@@ -94,11 +94,12 @@ class Timer:
                 fn()
         torch.cuda.synchronize()
         times = [[] for _ in fns]
-        per = max(1, steps // rounds)
-        for _ in range(rounds):
+        # exactly `steps` timed steps per method, spread over the rounds
+        counts = [steps // rounds + (1 if r < steps % rounds else 0) for r in range(rounds)]
+        for r in range(rounds):
             for m, fn in enumerate(fns):
                 evs = []
-                for _ in range(per):
+                for _ in range(counts[r]):
                     self.flush()
                     e0 = torch.cuda.Event(enable_timing=True)
                     e1 = torch.cuda.Event(enable_timing=True)
@@ -124,9 +125,11 @@ def streamk_runner(bt, t, stream):
     return fn, plan, ws
 
 
-def uniform_runner(bt, t, stream):
+def uniform_runner(bt, t, stream, force_chunks=0):
+    """decode_attention (the reference-shaped uniform split); force_chunks=1 is the reference's
+    "no split" row (one chunk, i.e. one workgroup item, per sequence and kv head)."""
     import pdattn
-    nc, ct = pdattn.plan_chunks(bt.G, bt.B, bt.Hkv, bt.max_len)
+    nc, ct = pdattn.plan_chunks(bt.G, bt.B, bt.Hkv, bt.max_len, force_chunks)
     p = pdattn.make_params(t["q"], t["k"], t["v"], t["indptr"], t["indices"], t["last"],
                            bt.B, bt.Hq, bt.Hkv, nc, ct)
     ws = pdattn.Workspace()
@@ -243,7 +246,9 @@ def cpu_baseline(bt_lens, Hq, Hkv, seed, budget_s=10.0):
     import oracle
     from pdattn import inputs
     bt = inputs.make_batch(bt_lens, Hq, Hkv, seed)
-    threads = min(16, os.cpu_count() or 1)
+    host_cores = os.cpu_count() or 1
+    # the box's CPU share for one GPU is 16 cores, whatever os.cpu_count() reports there
+    threads = min(16, host_cores)
     runs, t0 = 0, time.perf_counter()
     while True:
         oracle.decode(bt.q, bt.k, bt.v, bt.indptr, bt.indices, bt.last, Hq, Hkv, threads=threads)
@@ -262,38 +267,114 @@ def cpu_baseline(bt_lens, Hq, Hkv, seed, budget_s=10.0):
             break
     per1 = el1 / runs1
     return {"value": round(bt.algorithmic_bytes() / per / 1e9, 3), "unit": "GB/s",
-            "cores": threads, "kind": "port",
+            "cores": threads, "kind": "port", "host_cpu_count": host_cores,
             "sample": f"full B={bt.B} L={bt_lens[0]} workload, fp64 oracle (oracle/pdattn_oracle.c) "
-                      f"x{runs} runs, {per * 1e3:.1f} ms/run on {threads} threads",
+                      f"x{runs} runs, {per * 1e3:.1f} ms/run on {threads} threads ({threads} of the "
+                      f"{host_cores} CPUs os.cpu_count() reports: the box's share for one GPU)",
             "value_1_thread": round(bt.algorithmic_bytes() / per1 / 1e9, 3),
             "sample_1_thread": f"same workload x{runs1} runs, {per1 * 1e3:.1f} ms/run on 1 thread"}
 
 
-def decode_workload(timer, lens, args, with_uniform):
-    """Median cold step (flush before each), kernel duration (rotated back-to-back), plan info."""
+def decode_workload(timer, lens, args, with_uniform, seed=11, nosplit=False):
+    """Median cold step (flush before each) of the plan/run path, and of decode_attention (the
+    uniform split) and its one-chunk "no split" form beside it; the plan path's kernel duration
+    (rotated back to back); plan info."""
     import torch
     s = timer.stream
-    bt, t = make_device_batch(lens, 32, 8, seed=11)
+    bt, t = make_device_batch(lens, 32, 8, seed=seed)
     fn_sk, plan, ws = streamk_runner(bt, t, s)
-    fns = [fn_sk]
+    fns, keep = [fn_sk], []
     if with_uniform:
-        fn_un, keep_un, nc = uniform_runner(bt, t, s)
+        fn_un, k_un, nc = uniform_runner(bt, t, s)
         fns.append(fn_un)
+        keep.append(k_un)
+    if nosplit:
+        fn_ns, k_ns, nc1 = uniform_runner(bt, t, s, force_chunks=1)
+        fns.append(fn_ns)
+        keep.append(k_ns)
     times = timer.run(fns, args.steps, args.warmup, rounds=3)
     nbytes = bt.algorithmic_bytes()
     ms = statistics.median(times[0])
     kern_us, k, ncopy = rotated_kernel_us(plan, ws, t, s, args.steps)
     info = plan.info()
     r = {"bytes": nbytes, "ms": ms, "steps": len(times[0]), "kernel_us": kern_us,
-         "kernel_launches": k, "kv_copies": ncopy, "workgroups": info.workgroups}
+         "kernel_launches": k, "kv_copies": ncopy, "workgroups": info.workgroups,
+         "split_pairs": info.split_pairs}
     if with_uniform:
         mu = statistics.median(times[1])
         r["uniform"] = {"us_per_step": round(mu * 1e3, 2), "chunks": nc,
                         "GB/s": round(nbytes / (mu * 1e-3) / 1e9, 1)}
-        del keep_un
-    del t, ws
+    if nosplit:
+        mn = statistics.median(times[-1])
+        r["no_split"] = {"us_per_step": round(mn * 1e3, 2), "chunks": nc1,
+                         "items": nc1 * bt.B * bt.Hkv, "GB/s": round(nbytes / (mn * 1e-3) / 1e9, 1),
+                         "path": "decode_attention, force_chunks = 1"}
+    del keep, t, ws
     torch.cuda.empty_cache()
     return r
+
+
+def decode_leg(timer, lens, args, ceil, seed=11, reference=None):
+    """One decode configuration as a bench line: cold step, kernel time, both decode paths and the
+    no-split row, as % of 8 TB/s and of the measured streaming ceiling."""
+    h = decode_workload(timer, lens, args, with_uniform=True, seed=seed, nosplit=True)
+    v, a = gbs(h["bytes"], h["ms"] * 1e-3), gbs(h["bytes"], h["kernel_us"] * 1e-6)
+    out = {"B": len(lens), "L_mean": round(sum(lens) / len(lens), 1), "L_max": max(lens),
+           "algorithmic_bytes": h["bytes"], "workgroups": h["workgroups"], "split_pairs": h["split_pairs"],
+           "us_per_step": round(h["ms"] * 1e3, 2), "GB/s": round(v, 1),
+           "pct_of_peak": round(100 * v / PEAK_GBS, 1), "pct_of_ceiling": round(100 * v / ceil, 1),
+           "kernel_us": round(h["kernel_us"], 2), "kernel_GB/s": round(a, 1),
+           "kernel_pct_of_peak": round(100 * a / PEAK_GBS, 1),
+           "kernel_pct_of_ceiling": round(100 * a / ceil, 1),
+           "uniform_path": h["uniform"], "no_split": h["no_split"]}
+    for leg in (out["uniform_path"], out["no_split"]):
+        leg["pct_of_peak"] = round(100 * leg["GB/s"] / PEAK_GBS, 1)
+        leg["pct_of_ceiling"] = round(100 * leg["GB/s"] / ceil, 1)
+    if reference:
+        out["reference_published"] = reference
+    return out
+
+
+# The reference's published perf runs (results/01_decode_attention.txt:99-121, RTX 5060 Laptop,
+# 384 GB/s theoretical, 336 GB/s measured ceiling): its best split-KV variant and its no-split row.
+REF_DECODE = {
+    "1x32K": {"best_ms": 0.4134, "best_pct_of_peak": 84.6, "no_split_ms": 2.7655},
+    "8x8K": {"best_ms": 0.9032, "best_pct_of_peak": 77.4, "no_split_ms": 0.9032},
+    "64x1K": {"best_ms": 0.7925, "best_pct_of_peak": 88.5, "no_split_ms": 0.8250},
+}
+REF_CASCADE = {(64, 4096, 256): 2.34, (32, 16384, 512): 4.72, (8, 16384, 512): 2.20}
+
+
+def cascade_shape_leg(timer, args, B, Lp, Ls):
+    """One of the reference's shared-prefix perf shapes (01_decode_attention.cu:871-875): B requests
+    sharing an Lp-token prefix plus Ls private tokens each. The cascade against both non-shared
+    paths, same cold-cache method; the reference compares its cascade with its own non-shared
+    decode_attention."""
+    import pdattn
+    from pdattn import inputs
+    s = timer.stream
+    bt, t = make_device_batch(None, 32, 8, seed=21, shared_prefix=Lp, suffix=[Ls] * B)
+    f_plan, plan, ws = streamk_runner(bt, t, s)
+    f_uni, keep, nc = uniform_runner(bt, t, s)
+    base = pdattn.make_params(t["q"], t["k"], t["v"], t["indptr"], t["indices"], t["last"], bt.B, 32, 8)
+    cp = pdattn.CascadePlan(base, bt.indptr, bt.indices, bt.lens, t["indices"])
+    cws = pdattn.Workspace()
+    cp.decode(t["out"], t["lse"], cws, s)
+    f_cas = lambda: cp.decode(t["out"], t["lse"], cws, s)  # noqa: E731
+    wu, wp, wc = timer.run([f_uni, f_plan, f_cas], args.steps, args.warmup, rounds=3)
+    mu, mp, mc = (statistics.median(w) * 1e3 for w in (wu, wp, wc))
+    ci = cp.info()
+    ub = inputs.unique_bytes(bt)
+    out = {"cascade_us": round(mc, 2), "non_shared_uniform_us": round(mu, 2),
+           "non_shared_plan_us": round(mp, 2), "speedup_vs_uniform": round(mu / mc, 2),
+           "speedup_vs_plan": round(mp / mc, 2), "reference_speedup": REF_CASCADE.get((B, Lp, Ls)),
+           "unique_bytes": ub, "cascade_GB/s_unique": round(gbs(ub, mc * 1e-6), 1),
+           "mode": {0: "fused", 1: "serial", 2: "two_streams"}[ci.mode],
+           "prefix_chunks": ci.prefix_chunks, "prefix_workgroups": ci.prefix_workgroups}
+    cp.close()
+    pdattn.workspace_release(cws)
+    del t, ws, keep
+    return out
 
 
 def gbs(nbytes, seconds):
@@ -552,10 +633,24 @@ def main():
     if args.only == "tree":
         print(json.dumps({"cascade_tree": tree_workload(timer, args)}))
         return
+    if args.only == "legs":
+        from pdattn import inputs
+        ceil = ceiling_gbs(timer, args.steps)
+        out = {"stream_read_ceiling_GBs": round(ceil, 1)}
+        for tag, lens_i, seed in [("C1 1x2K", [2048], 11), ("C3 8x8K", [8192] * 8, 11),
+                                  ("C4 ragged B=64 L~U[256,4096]", inputs.ragged_lens(64, 256, 4096, seed=17), 17)]:
+            out[tag] = decode_leg(timer, lens_i, args, ceil, seed=seed)
+        out["cascade_reference_shapes"] = {
+            f"{B}x({Lp}+{Ls})": cascade_shape_leg(timer, args, B, Lp, Ls) for (B, Lp, Ls) in REF_CASCADE}
+        print(json.dumps(out))
+        return
     lens = [1024] * 64 if args.only == "64x1k" else [32768]
     name = ("paged GQA decode B=64 L=1024 (metric's 64x1K)" if args.only == "64x1k"
             else "paged GQA decode B=1 L=32768 (configs[1])")
-    h = decode_workload(timer, lens, args, with_uniform=args.only in ("", "32k", "64x1k"))
+    full = not args.only and not args.no_secondary
+    ceil = ceiling_gbs(timer, args.steps) if full else None
+    h = decode_workload(timer, lens, args, with_uniform=args.only in ("", "32k", "64x1k"),
+                        nosplit=args.only in ("", "32k", "64x1k"))
     value = gbs(h["bytes"], h["ms"] * 1e-3)
     achieved = gbs(h["bytes"], h["kernel_us"] * 1e-6)
     traffic = measured_traffic() if not args.only or args.only == "32k" else None
@@ -571,17 +666,21 @@ def main():
                 "timing": "median of per-step HIP events, 1 GiB read flush before each step"},
         roofline={"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                   "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
-                  "kernel": "decode_balanced_kernel (+ merge_split_kernel when pairs are split)",
+                  "traffic_source": (f"{os.path.relpath(TRAFFIC_FILE, ROOT)}: rocprofv3 --pmc FETCH_SIZE / "
+                                     "WRITE_SIZE of the decode launch, copy-calibrated" if traffic else None),
+                  "kernel": "one decode step = decode_balanced_kernel + merge_split_kernel (the merge "
+                            "launch runs when pairs are split); frac is the whole step's, both launches",
                   "kernel_us": round(h["kernel_us"], 2),
-                  "timing": f"{h['kernel_launches']} back-to-back launches over {h['kv_copies']} "
+                  "timing": f"{h['kernel_launches']} back-to-back steps over {h['kv_copies']} "
                             f"K/V copies (>= 1 GiB) between one event pair"},
         device={"arch": dinfo.arch.decode(), "cus": dinfo.compute_units},
     )
     if "uniform" in h:
         result["uniform_path"] = h["uniform"]
-    if not args.only and not args.no_secondary:
+    if "no_split" in h:
+        result["no_split"] = h["no_split"]
+    if full:
         sec = {}
-        ceil = ceiling_gbs(timer, args.steps)
         result["stream_read_ceiling_GBs"] = round(ceil, 1)
         result["pct_of_ceiling"] = round(100 * value / ceil, 1)
         result["roofline"]["frac_of_ceiling"] = round(achieved / ceil, 4)
@@ -591,20 +690,26 @@ def main():
             "kernel_frac": round(sm_us / h["kernel_us"], 4),
             "what": "stream_read over the workload's algorithmic bytes in one launch, back to back "
                     "over rotated buffers (>= 1 GiB); kernel_frac = its time / the decode step's"}
-        h2 = decode_workload(timer, [1024] * 64, args, with_uniform=True)
-        v2, a2 = gbs(h2["bytes"], h2["ms"] * 1e-3), gbs(h2["bytes"], h2["kernel_us"] * 1e-6)
-        sm2_us = size_matched_read_us(h2["bytes"], timer.stream, args.steps)
-        sec["64x1K"] = {"us_per_step": round(h2["ms"] * 1e3, 2), "GB/s": round(v2, 1),
-                        "pct_of_peak": round(100 * v2 / PEAK_GBS, 1),
-                        "pct_of_ceiling": round(100 * v2 / ceil, 1),
-                        "kernel_us": round(h2["kernel_us"], 2), "kernel_GB/s": round(a2, 1),
-                        "kernel_frac_of_ceiling": round(a2 / ceil, 4),
-                        "size_matched_read_us": round(sm2_us, 2),
-                        "kernel_frac_of_size_matched_read": round(sm2_us / h2["kernel_us"], 4),
-                        "workgroups": h2["workgroups"], "algorithmic_bytes": h2["bytes"],
-                        "uniform_path": h2["uniform"]}
+        result["reference_published"] = REF_DECODE["1x32K"]
+        for sub in (result.get("no_split"), result.get("uniform_path")):
+            if sub:
+                sub["pct_of_peak"] = round(100 * sub["GB/s"] / PEAK_GBS, 1)
+                sub["pct_of_ceiling"] = round(100 * sub["GB/s"] / ceil, 1)
+        from pdattn import inputs
+        legs = [("64x1K", [1024] * 64, 11), ("C1 1x2K", [2048], 11), ("C3 8x8K", [8192] * 8, 11),
+                ("C4 ragged B=64 L~U[256,4096]", inputs.ragged_lens(64, 256, 4096, seed=17), 17)]
+        for tag, lens_i, seed in legs:
+            leg = decode_leg(timer, lens_i, args, ceil, seed=seed,
+                             reference=REF_DECODE.get(tag.split()[-1] if tag != "64x1K" else "64x1K"))
+            if tag == "64x1K":
+                sm2_us = size_matched_read_us(leg["algorithmic_bytes"], timer.stream, args.steps)
+                leg["size_matched_read_us"] = round(sm2_us, 2)
+                leg["kernel_frac_of_size_matched_read"] = round(sm2_us / leg["kernel_us"], 4)
+            sec[tag] = leg
         sec["cascade_64x(8192+512)"] = cascade_workload(timer, args)
         sec["cascade_64x(8192+512)_G8"] = cascade_workload(timer, args, 64, 8)
+        sec["cascade_reference_shapes"] = {
+            f"{B}x({Lp}+{Ls})": cascade_shape_leg(timer, args, B, Lp, Ls) for (B, Lp, Ls) in REF_CASCADE}
         sec["cascade_prefix_mfma"] = prefix_workload(timer, args)
         sec["append_kv"] = append_workload(timer, args)
         sec["hip_graph"] = graph_workload(timer, args)

@@ -285,15 +285,16 @@ struct pdattn_cascade_plan {
 
 namespace {
 
-// Balanced split; see pdattn.h and pdattn_internal.h. Chunks of up to P pages of one (sequence,
-// kv head) pair are ordered sequence-major, then by chunk position, kv head fastest, so that any
-// stretch of the order mixes all kv heads (whose K/V rows sit at different offsets of every page,
-// which the memory system serves at different rates). Workgroup w owns the units
-// [U w / W, U (w+1) / W) of that order; the walk below cuts each range into one segment per chunk
-// piece. The contributors of a pair are its segments in unit order; a pair with more than one
-// (or every pair, when `merge_all` is set for extra partials) gets consecutive partial slots and
-// an entry in the merge list. W grows (doubling) until every workgroup has at most seg_cap
-// (<= kSegMax) segments and kRangeMax pages.
+// Balanced split; see pdattn.h and pdattn_internal.h. Default: page ranges shared by the Hkv
+// workgroups of a group (one kv head each), so that the token rows of a page are read whole.
+// Otherwise (a forced chunk size, or a grid that is not a multiple of Hkv): chunks of up to P
+// pages of one (sequence, kv head) pair, ordered sequence-major, then by chunk position, kv head
+// fastest, and workgroup w owns the units [U w / W, U (w+1) / W) of that order. Either walk cuts
+// each workgroup's range into one segment per sequence (or chunk) piece. The contributors of a
+// pair are its segments in page order; a pair with more than one (or every pair, when `merge_all`
+// is set for extra partials) gets consecutive partial slots and an entry in the merge list. W
+// grows (doubling) until every workgroup has at most seg_cap (<= kSegMax) segments and kRangeMax
+// pages.
 int build_balanced_plan(const int32_t* indptr, const int32_t* last, int B, int Hq, int Hkv,
                         int force_wg, int chunk_pages, bool merge_all, pdattn_plan* pl,
                         int seg_cap = 0) {
@@ -327,19 +328,79 @@ int build_balanced_plan(const int32_t* indptr, const int32_t* last, int B, int H
         // whose workgroups share the CUs with the prefix pass
         W = (int64_t)f.cus * (wide && !merge_all ? 2 : 1);
     }
-    W = std::max<int64_t>(1, std::min<int64_t>(W, std::max<int64_t>(1, pl->U)));
-    W = std::max<int64_t>(W, (pl->U + kRangeMax - 1) / kRangeMax);
+    // Page-range groups, the default: the pages of all sequences, in page-table order, are cut
+    // into NG = W / Hkv equal ranges, and workgroup g * Hkv + h takes range g for kv head h. The
+    // Hkv workgroups of a group stream the same pages at the same time, each its own 256-byte
+    // column of every 2 KB token row, so each token row of K and V is read whole while it is open
+    // in DRAM. A forced chunk size, or a grid that is not a multiple of Hkv, uses the unit ranges
+    // below instead (chunks of one kv head, kv head fastest).
+    const bool grouped = chunk_pages == 0 && W >= Hkv && W % Hkv == 0;
+    if (!grouped) {
+        W = std::max<int64_t>(1, std::min<int64_t>(W, std::max<int64_t>(1, pl->U)));
+        W = std::max<int64_t>(W, (pl->U + kRangeMax - 1) / kRangeMax);
+    }
     if (W > (1 << 28)) return fail(PDATTN_ERR_INVALID_ARGUMENT, "grid too large");
 
     const int64_t U = pl->U;
     const int P = pl->P;
+    const int64_t nnz = pl->nnz;
+    const int jbase = pl->jbase;
     auto seq_len = [&](int b) { return (indptr[b + 1] - indptr[b] - 1) * kPage + last[b]; };
     const size_t pairs = (size_t)B * Hkv;
     struct SegRef { int64_t w; int idx; size_t pair; };
     std::vector<int32_t> desc;
     std::vector<SegRef> refs;
     std::vector<int> nc;
-    for (;;) {
+    // appends segment {b, kvh, pages [p0, p1) of sequence b} to workgroup w, whose page list starts
+    // at page-table position wbeg (relative to kv_indptr[0]); false when w is full
+    auto add_segment = [&](int64_t w, int64_t wbeg, int b, int kvh, int p0, int p1) {
+        int32_t* d = &desc[(size_t)w * kBalDescInts];
+        if (d[0] == seg_cap) return false;
+        int32_t* sg = d + 8 + kSegInts * d[0];
+        const int np = indptr[b + 1] - indptr[b];
+        const int64_t pos = indptr[b] - jbase + p0;
+        sg[0] = b;
+        sg[1] = kvh;
+        sg[2] = (int)(pos - wbeg);
+        sg[3] = p1 - p0;
+        sg[4] = p0 * kPage;
+        sg[5] = p1 == np ? seq_len(b) : p1 * kPage;
+        sg[6] = (int)pos;
+        sg[7] = -1;
+        const size_t pr = (size_t)b * Hkv + kvh;
+        refs.push_back({w, d[0], pr});
+        ++nc[pr];
+        ++d[0];
+        return true;
+    };
+    if (grouped) {
+        int64_t NG = std::min<int64_t>(W / Hkv, std::max<int64_t>(1, nnz));
+        for (;;) {
+            W = NG * Hkv;
+            desc.assign((size_t)W * kBalDescInts, 0);
+            refs.clear();
+            nc.assign(pairs, 0);
+            bool ok = true;
+            int b = 0;
+            for (int64_t g = 0; g < NG && ok; ++g) {
+                const int64_t lo = nnz * g / NG, hi = nnz * (g + 1) / NG;
+                if (hi - lo > kRangeMax) { ok = false; break; }
+                while (b < B && indptr[b + 1] - jbase <= lo) ++b;   // first sequence reaching past lo
+                for (int bb = b; bb < B && indptr[bb] - jbase < hi && ok; ++bb) {
+                    const int64_t s0 = std::max<int64_t>(lo, indptr[bb] - jbase);
+                    const int64_t s1 = std::min<int64_t>(hi, indptr[bb + 1] - jbase);
+                    if (s1 <= s0) continue;   // an empty sequence
+                    const int p0 = (int)(s0 - (indptr[bb] - jbase)), p1 = (int)(s1 - (indptr[bb] - jbase));
+                    for (int kvh = 0; kvh < Hkv && ok; ++kvh) ok = add_segment(g * Hkv + kvh, lo, bb, kvh, p0, p1);
+                }
+            }
+            if (ok) break;
+            if (NG >= std::max<int64_t>(1, nnz)) return fail(PDATTN_ERR_INVALID_ARGUMENT, "cannot partition the batch");
+            NG = std::min<int64_t>(std::max<int64_t>(1, nnz), NG * 2);
+        }
+        pl->P = (int)((nnz + W / Hkv - 1) / (W / Hkv));   // pages per range
+    }
+    for (; !grouped;) {
         desc.assign((size_t)W * kBalDescInts, 0);
         refs.clear();
         nc.assign(pairs, 0);

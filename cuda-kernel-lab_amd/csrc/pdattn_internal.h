@@ -31,11 +31,10 @@ struct PartialArgs {
     float scale_log2;         // sm_scale * log2(e)
 };
 
-// Balanced decode: the host planner cuts the batch into chunks of up to `chunk_pages` pages of
-// one (sequence, kv head) pair, ordered sequence-major, then by chunk position, with the kv head
-// varying fastest, and gives workgroup w the units [U w / W, U (w+1) / W) of that order (a unit is
-// one page of one kv head). Each workgroup's range is cut into segments (one per chunk piece),
-// described in desc[w * kBalDescInts ..]:
+// Balanced decode: the host planner gives each workgroup a range of pages of one kv head -- by
+// default range g of the page sequence cut into W / Hkv equal ranges for workgroup g * Hkv + h,
+// kv head h; or the units [U w / W, U (w+1) / W) of the pairs' chunks, kv head fastest -- cut into
+// segments (one per sequence or chunk piece), described in desc[w * kBalDescInts ..]:
 //   desc[0] = number of segments; segment s at desc[8 + kSegInts * s] =
 //   {b, kvh, qa, npg, t0, t1, jpos, slot}: sequence b, kv head kvh, pages [qa, qa + npg) of the
 //   workgroup's page list, tokens [t0, t1) of the sequence (t0 = first token of its first page),

@@ -149,15 +149,17 @@ int pdattn_decode_attention_noalloc(const pdattn_decode_params* p, int G, int va
 
 /* ---- balanced path (plan / run) ---------------------------------------------------------- */
 /* The MI355X path for decode_attention. The planner works on the host, from the host copy of the
- * page table, the way FlashInfer's plan() does. It cuts every (sequence, kv head) pair into chunks
- * of up to chunk_pages pages and orders them sequence-major, then by chunk position, with the kv
- * head varying fastest. It then gives each workgroup of a single launch (one per CU) an equal
- * range of that order, so every workgroup streams the same number of pages over a mix of kv heads.
+ * page table, the way FlashInfer's plan() does. It cuts the pages of all sequences, taken in
+ * page-table order, into W / Hkv equal ranges, and gives workgroup g * Hkv + h of a single launch
+ * (W = one per CU) range g for kv head h: every workgroup streams the same number of pages, and
+ * the Hkv workgroups of a range read the same pages at the same time, each its own 256-byte column
+ * of every 2 KB token row, so each token row is read whole while it is open in DRAM. A range that
+ * holds pieces of several sequences gives its workgroups one segment per piece.
  *
- * A pair that lies in one workgroup's range is written as the final out / lse by that workgroup.
- * The pieces of a pair split over several workgroups are written as normalized partials and
- * merged by a second, small launch, in a fixed order. The result is bitwise deterministic for a
- * given plan. */
+ * A (sequence, kv head) pair that lies in one workgroup's range is written as the final out / lse
+ * by that workgroup. The pieces of a pair split over several workgroups are written as normalized
+ * partials and merged by a second, small launch, in a fixed order. The result is bitwise
+ * deterministic for a given plan. */
 typedef struct pdattn_plan pdattn_plan;
 
 typedef struct pdattn_plan_info {
@@ -167,16 +169,20 @@ typedef struct pdattn_plan_info {
     int     max_contributors;  /* most segments contributing to one pair                  */
     int64_t units;             /* Hkv * nnz page units                                    */
     size_t  workspace_bytes;
-    int     chunk_pages;       /* pages per chunk                                         */
+    int     chunk_pages;       /* pages per chunk, or per range of the default partition */
     int     segments;          /* segments over all workgroups                            */
     int     merge_entries;     /* pairs merged by the second launch (0: single launch)    */
     int     schedule_ints;     /* int32 count of pdattn_plan_get_schedule's output        */
 } pdattn_plan_info;
 
 /* Build a plan from host copies of kv_indptr [B+1] and kv_last_page_len [B]. force_workgroups > 0
- * overrides the grid size (one workgroup per CU by default; it is clamped to the number of page
- * units, and grows when a workgroup would exceed its segment or page limits); chunk_pages > 0
- * overrides the chunk size (default 64 pages). */
+ * overrides the grid size (one workgroup per CU by default, two at G = 8; it grows when a
+ * workgroup would exceed its segment or page limits). chunk_pages > 0, or a grid that is not a
+ * multiple of Hkv, selects the other partition: chunks of up to chunk_pages pages (64 by default)
+ * of one (sequence, kv head) pair, ordered sequence-major, then by chunk position, kv head
+ * fastest, with workgroup w taking the page units [U w / W, U (w+1) / W) of that order (U = Hkv *
+ * nnz; the grid is then clamped to U). info.chunk_pages reports the chunk size, or the pages per
+ * range of the default partition. */
 int pdattn_plan_create(const int32_t* h_kv_indptr, const int32_t* h_kv_last_page_len, int B,
                        int Hq, int Hkv, int force_workgroups, int chunk_pages, pdattn_plan** plan);
 int pdattn_plan_get_info(const pdattn_plan* plan, pdattn_plan_info* info);

@@ -112,6 +112,76 @@ def test_schedule_matches_contract(lens, Hkv, W, P):
     assert len(seen) == U
 
 
+def brute_grouped(indptr, last, Hkv, W):
+    """The page-range partition (chunk_pages = 0): the nnz pages, in page-table order, are cut into
+    NG = W / Hkv ranges [nnz g / NG, nnz (g+1) / NG); workgroup g Hkv + h takes range g for kv
+    head h, one segment per sequence piece in the range."""
+    B = len(indptr) - 1
+    jbase = int(indptr[0])
+    nnz = int(indptr[-1]) - jbase
+    NG = W // Hkv
+    segs = [[] for _ in range(W)]
+    for g in range(NG):
+        lo, hi = nnz * g // NG, nnz * (g + 1) // NG
+        for b in range(B):
+            start, end = int(indptr[b]) - jbase, int(indptr[b + 1]) - jbase
+            s0, s1 = max(lo, start), min(hi, end)
+            if s1 <= s0:
+                continue
+            p0, p1, np_ = s0 - start, s1 - start, end - start
+            t1 = (np_ - 1) * 16 + int(last[b]) if p1 == np_ else p1 * 16
+            for kvh in range(Hkv):
+                segs[g * Hkv + kvh].append([b, kvh, s0 - lo, p1 - p0, p0 * 16, t1, s0, -1])
+    contrib = {}
+    for w, ss in enumerate(segs):
+        for k, sg in enumerate(ss):
+            contrib.setdefault((sg[0], sg[1]), []).append((w, k))
+    merge, slot = [], 0
+    for b in range(B):
+        for kvh in range(Hkv):
+            cs = contrib.get((b, kvh), [])
+            if len(cs) > 1:
+                for k, (w, i) in enumerate(cs):
+                    segs[w][i][7] = slot + k
+                merge.append([b, kvh, slot, len(cs)])
+                slot += len(cs)
+            elif not cs:
+                merge.append([b, kvh, 0, 0])
+    return segs, merge
+
+
+@pytest.mark.parametrize("lens,Hkv", CASES, ids=[f"{len(c[0])}seq-{c[1]}kv" for c in CASES])
+@pytest.mark.parametrize("W", [8, 64, 256, 512, 1000])
+def test_grouped_schedule_matches_contract(lens, Hkv, W):
+    """The default partition: every page of every kv head exactly once, and the Hkv workgroups of a
+    group hold the same page ranges (they stream whole token rows together)."""
+    bt = inputs.make_batch(lens, Hkv * 4, Hkv, seed=1, fill=False)
+    if bt.indptr[-1] == 0:
+        pytest.skip("no pages")
+    if W % Hkv:
+        pytest.skip("grid not a multiple of Hkv")
+    plan = pdattn.Plan(bt.indptr, bt.last, bt.B, Hkv * 4, Hkv, force_workgroups=W)
+    info = plan.info()
+    Wp = info.workgroups
+    assert Wp % Hkv == 0
+    segs, merge = brute_grouped(bt.indptr, bt.last, Hkv, Wp)
+    got_segs, got_merge = plan.schedule()
+    assert got_segs == segs
+    assert got_merge.tolist() == merge
+    for g in range(Wp // Hkv):
+        ranges = [[(s[0], s[2], s[3], s[6]) for s in got_segs[g * Hkv + h]] for h in range(Hkv)]
+        assert all(r == ranges[0] for r in ranges)
+        assert all(s[1] == h for h in range(Hkv) for s in got_segs[g * Hkv + h])
+        assert len(got_segs[g * Hkv]) <= pdattn.SCHEDULE_SEGMENTS
+    seen = set()
+    for ss in got_segs:
+        for b, kvh, qa, npg, t0, t1, jpos, slot in ss:
+            for i in range(npg):
+                assert (kvh, jpos + i) not in seen
+                seen.add((kvh, jpos + i))
+    assert len(seen) == info.units
+
+
 def test_every_workgroup_mixes_kv_heads():
     """One long sequence: every workgroup's range covers several kv heads (the order's purpose)."""
     bt = inputs.make_batch([32768], 32, 8, seed=1, fill=False)
