@@ -241,6 +241,7 @@ int ensure_ws(pdattn_workspace* ws, size_t need) {
 struct pdattn_plan {
     int B = 0, Hq = 0, Hkv = 0, G = 0;
     int nnz = 0, jbase = 0, W = 1, P = 16;
+    int ngroups = 0;                  // > 0: page-range partition of that many groups
     int64_t U = 0;
     int split_pairs = 0, max_contrib = 0, n_entries = 0, n_slots = 0, segments = 0;
     // workspace layout (bytes from the base)
@@ -399,6 +400,7 @@ int build_balanced_plan(const int32_t* indptr, const int32_t* last, int B, int H
             NG = std::min<int64_t>(std::max<int64_t>(1, nnz), NG * 2);
         }
         pl->P = (int)((nnz + W / Hkv - 1) / (W / Hkv));   // pages per range
+        pl->ngroups = (int)(W / Hkv);
     }
     for (; !grouped;) {
         desc.assign((size_t)W * kBalDescInts, 0);
@@ -543,6 +545,8 @@ BalArgs bal_args(const pdattn_plan* pl, const void* q, const void* k, const void
     a.W = pl->W;
     a.scale_log2 = sm_scale * 1.4426950408889634f;
     a.part_stride = 0;   // the planner's slot-major partials
+    a.ngroups = pl->ngroups;
+    a.nnz = pl->nnz;
     return a;
 }
 
@@ -929,6 +933,8 @@ static int launch_uniform_split(const PartialArgs& a, int G, hipStream_t s) {
     d.W = (int)((n_items + per - 1) / per);
     d.scale_log2 = a.scale_log2;
     d.part_stride = a.part_stride;
+    d.ngroups = 0;
+    d.nnz = 0;
     u.kv_indptr = a.kv_indptr;
     u.kv_last = a.kv_last;
     u.kv_start = a.kv_start;

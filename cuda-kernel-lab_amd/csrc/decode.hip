@@ -709,14 +709,15 @@ struct BalShared {
     BalSmem<C::G, C::NW * C::RPI, HP> sm;
     int pg[kRangeMax];                             // the workgroup's page ids
     u32x4 qs[SEGS][C::G * kHeadDim / 8];           // q rows of each segment
-    int sd[kSegMax * kSegInts];                    // segment descriptors
+    int sd[kBalDescInts];                          // descriptor block: header, then segments
 };
 
 // The body of one balanced-decode workgroup w (the kernel's argument block must start with the
 // BalArgs `a`, which kargs() reads).
-template <class C, bool UNI = false, bool COMPACT = false>
+template <class C, bool UNI = false, bool COMPACT = false, bool RANGES = false>
 __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COMPACT>& S, int w,
                                               const UniArgs* u = nullptr) {
+    static_assert(!(UNI && RANGES), "the uniform split builds its own descriptors");
     constexpr int G = C::G, NW = C::NW, NT = C::NT, NBUF = C::NBUF, LPR = C::LPR;
     auto& sm = S.sm;
     int* pg = S.pg;
@@ -729,14 +730,43 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
     const int r = lane / LPR, c = lane % LPR;
     // Segment fields are staged in LDS and read back wave-uniform: global (vector) loads of them
     // would count against the same wait counter as the ring's page loads, and a non-uniform value
-    // in a buffer resource would turn every page load into a loop over lanes.
-    auto fld = [&](int si, int f) { return __builtin_amdgcn_readfirstlane(sd[si * kSegInts + f]); };
+    // in a buffer resource would turn every page load into a loop over lanes. sd holds the
+    // descriptor block: a header of 8 ints, then the segments.
+    int* seg = sd + 8;
+    auto fld = [&](int si, int f) { return __builtin_amdgcn_readfirstlane(seg[si * kSegInts + f]); };
+    constexpr int PMAX = kRangeMax / NT, QPS = G * kHeadDim / 8;
+    constexpr int QMAX = (BalShared<C, COMPACT>::SEGS * QPS + NT - 1) / NT;
+    // A page-range plan (RANGES: ngroups > 0) gives workgroup w = g * Hkv + kvh the pages
+    // [lo, hi) of the page table (relative to kv_indptr[0]), lo = nnz g / ngroups: its page list is
+    // known from the kernel arguments, so the page ids are loaded together with the descriptor
+    // block, and the ring's first pages together with the q rows.
+    int64_t lo = 0, hi = 0;
+    if constexpr (RANGES) {
+        const int64_t g = w / a.Hkv, nnz = kargs()->nnz, ng = kargs()->ngroups;
+        lo = nnz * g / ng;
+        hi = nnz * (g + 1) / ng;
+    }
     int nseg;
     if constexpr (!UNI) {
+        // round trip 1: the whole descriptor block (one int per thread), and the page ids of a
+        // page-range plan
         const int32_t* desc = kargs()->desc + (size_t)w * kBalDescInts;
-        nseg = __builtin_amdgcn_readfirstlane(desc[0]);
-        if (nseg <= 0) return;   // uniform: the planner gives every workgroup at least one segment
-        for (int i = tid; i < nseg * kSegInts; i += NT) sd[i] = desc[8 + i];
+        const int32_t* kvi = kargs()->kv_indices + lo;   // (pointers read from the arguments once)
+        const int dv = tid < kBalDescInts ? desc[tid] : 0;
+        int pv[PMAX];
+        const int npr = (int)(hi - lo);
+#pragma unroll
+        for (int k = 0; k < PMAX; ++k) {
+            const int i = tid + k * NT;
+            pv[k] = i < npr ? kvi[i] : 0;
+        }
+        if (tid < kBalDescInts) sd[tid] = dv;
+#pragma unroll
+        for (int k = 0; k < PMAX; ++k)
+            if (tid + k * NT < npr) pg[tid + k * NT] = pv[k];
+        __syncthreads();
+        nseg = __builtin_amdgcn_readfirstlane(sd[0]);
+        if (nseg <= 0) return;   // uniform: every thread leaves
     } else {
         // items w, w + W, ...: thread t builds the descriptor of the t-th (the decode_partial
         // rule, 01_decode_attention.cu:88-97: keys [kv_start + chunk * chunk_tokens, + chunk_tokens)
@@ -754,7 +784,7 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
             const int kbeg = u->kv_start + chunk * u->chunk_tokens;
             const int kend = max(kbeg, min(len, kbeg + u->chunk_tokens));
             const int pf = kbeg / kPage;
-            int* sg = sd + tid * kSegInts;
+            int* sg = seg + tid * kSegInts;
             sg[0] = b;
             sg[1] = kvh;
             sg[3] = kend > kbeg ? (kend - 1) / kPage - pf + 1 : 0;
@@ -767,48 +797,11 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
         // page-list offsets: exclusive prefix sum of the page counts
         if (tid < nseg) {
             int qa = 0;
-            for (int j = 0; j < tid; ++j) qa += sd[j * kSegInts + 3];
-            sd[tid * kSegInts + 2] = qa;
+            for (int j = 0; j < tid; ++j) qa += seg[j * kSegInts + 3];
+            seg[tid * kSegInts + 2] = qa;
         }
+        __syncthreads();
     }
-    __syncthreads();
-    // page ids and q rows of every segment into LDS: all loads are issued before any is stored
-    // (one round trip, not one per segment). Item i < npages is page i of the workgroup's list,
-    // found in the segment whose range [qa, qa + npg) holds it; q item j is 16 bytes of the
-    // G q rows of segment j / (G*16).
-    {
-        constexpr int PMAX = kRangeMax / NT, QPS = G * kHeadDim / 8;
-        constexpr int QMAX = (BalShared<C, COMPACT>::SEGS * QPS + NT - 1) / NT;
-        const int npages = fld(nseg - 1, 2) + fld(nseg - 1, 3);
-        int pv[PMAX];
-        u32x4 qv4[QMAX];
-#pragma unroll
-        for (int k = 0; k < PMAX; ++k) {
-            const int i = tid + k * NT;
-            pv[k] = 0;
-            if (i < npages) {
-                int si = 0;
-                while (si + 1 < nseg && sd[(si + 1) * kSegInts + 2] <= i) ++si;
-                pv[k] = kargs()->kv_indices[sd[si * kSegInts + 6] + (i - sd[si * kSegInts + 2])];
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < QMAX; ++k) {
-            const int j = tid + k * NT;
-            if (j < nseg * QPS) {
-                const int si = j / QPS;
-                const size_t row = (size_t)sd[si * kSegInts] * a.Hq + (size_t)sd[si * kSegInts + 1] * G;
-                qv4[k] = reinterpret_cast<const u32x4*>(kargs()->q + row * kHeadDim)[j % QPS];
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < PMAX; ++k)
-            if (tid + k * NT < npages) pg[tid + k * NT] = pv[k];
-#pragma unroll
-        for (int k = 0; k < QMAX; ++k)
-            if (tid + k * NT < nseg * QPS) qs[(tid + k * NT) / QPS][(tid + k * NT) % QPS] = qv4[k];
-    }
-    __syncthreads();
 
     const uint32_t page_bytes = (uint32_t)(kPage * a.Hkv * 256);
     const uint32_t lbase = (uint32_t)(r * a.Hkv * 256 + c * 16);
@@ -825,7 +818,6 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
             ++ps;
         }
     };
-    seek();
     auto issue = [&](PageRegs<C>& buf) {
         const uint8_t* kb = kargs()->k;
         const uint8_t* vb = kargs()->v;
@@ -846,9 +838,66 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
         }
     };
 
+    // round trip 2: the q rows of every segment, the page ids of the other plans (item i of the
+    // workgroup's page list is found in the segment whose range [qa, qa + npg) holds it), and for
+    // a page-range plan the first pages of the ring, all issued before any is waited for
     PageRegs<C> buf[NBUF];
+    {
+        const int npages = fld(nseg - 1, 2) + fld(nseg - 1, 3);
+        const _Float16* qp = kargs()->q;
+        const int32_t* kvi = kargs()->kv_indices;
+        // page-table positions of the page list first (LDS reads only: a search loop with loads
+        // in flight would make the compiler wait for them at every iteration)
+        int src[PMAX];
+        if constexpr (!RANGES) {
 #pragma unroll
-    for (int u = 0; u < NBUF - 1; ++u) issue(buf[u]);
+            for (int k = 0; k < PMAX; ++k) {
+                const int i = tid + k * NT;
+                src[k] = -1;
+                if (i < npages) {
+                    int si = 0;
+                    while (si + 1 < nseg && seg[(si + 1) * kSegInts + 2] <= i) ++si;
+                    src[k] = seg[si * kSegInts + 6] + (i - seg[si * kSegInts + 2]);
+                }
+            }
+        }
+        // (every load is issued, past the last segment from segment 0's rows, so that the number
+        // of loads in flight is the same on every path and the waits below stay exact)
+        u32x4 qv4[QMAX];
+#pragma unroll
+        for (int k = 0; k < QMAX; ++k) {
+            const int j = tid + k * NT < nseg * QPS ? tid + k * NT : 0;
+            const int si = j / QPS;
+            const size_t row = (size_t)seg[si * kSegInts] * a.Hq + (size_t)seg[si * kSegInts + 1] * G;
+            qv4[k] = reinterpret_cast<const u32x4*>(qp + row * kHeadDim)[j % QPS];
+        }
+        int pv[PMAX];
+        if constexpr (!RANGES) {
+#pragma unroll
+            for (int k = 0; k < PMAX; ++k) pv[k] = kvi[max(src[k], 0)];   // (unconditional: one round trip)
+        } else {
+            seek();
+#pragma unroll
+            for (int u = 0; u < NBUF - 1; ++u) issue(buf[u]);
+        }
+        // keeps the stores below after the loads above: the q rows are waited for while the
+        // first pages are still in flight
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < QMAX; ++k)
+            if (tid + k * NT < nseg * QPS) qs[(tid + k * NT) / QPS][(tid + k * NT) % QPS] = qv4[k];
+        if constexpr (!RANGES) {
+#pragma unroll
+            for (int k = 0; k < PMAX; ++k)
+                if (tid + k * NT < npages) pg[tid + k * NT] = pv[k];
+        }
+    }
+    __syncthreads();
+    if constexpr (!RANGES) {
+        seek();
+#pragma unroll
+        for (int u = 0; u < NBUF - 1; ++u) issue(buf[u]);
+    }
 
     WaveState<C> st;
     reset_state<C>(st);
@@ -885,10 +934,10 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
 // memory time with one wave per SIMD, so the kernel uses the compact LDS layout (61 KB) and the
 // planner gives it two workgroups per CU: the two waves on each SIMD overlap one's arithmetic with
 // the other's loads.
-template <class C>
+template <class C, bool RANGES>
 __global__ __launch_bounds__(C::NT) void decode_balanced_kernel(BalArgs a) {
     __shared__ BalShared<C, (C::G > 4)> S;
-    balanced_body<C, false, (C::G > 4)>(a, S, blockIdx.x);
+    balanced_body<C, false, (C::G > 4), RANGES>(a, S, blockIdx.x);
 }
 
 // The reference-shaped uniform split on the balanced body (items of equal key ranges, descriptors
@@ -905,7 +954,7 @@ __global__ __launch_bounds__(C::NT) void decode_uniform_kernel(UniArgs u) {
 // one per CU, and the prefix blocks fill the second slots, so every CU streams suffix pages
 // while its matrix core works on the prefix. Partials of both go to the workspace and are merged
 // by the next launch.
-template <class C>
+template <class C, bool RANGES>
 __global__ __launch_bounds__(C::NT, 2) void cascade_step_kernel(StepArgs s) {
     static_assert(C::NT == kPrefixThreads, "both roles use the same workgroup shape");
     typedef BalShared<C, (C::G > 4)> Dec;   // G = 8: the compact layout (fits beside a prefix workgroup)
@@ -913,7 +962,7 @@ __global__ __launch_bounds__(C::NT, 2) void cascade_step_kernel(StepArgs s) {
     __shared__ __align__(16) unsigned char raw[SB];
     const int i = blockIdx.x;
     if (i < s.n_dec) {
-        balanced_body<C, false, (C::G > 4)>(s.d, *reinterpret_cast<Dec*>(raw), i);
+        balanced_body<C, false, (C::G > 4), RANGES>(s.d, *reinterpret_cast<Dec*>(raw), i);
     } else {
         const int j = i - s.n_dec, n_items = s.p.num_chunks;
         prefix_workgroup(s.p, *reinterpret_cast<PSmem*>(raw), j % n_items, 0, j / n_items);
@@ -948,7 +997,8 @@ void launch_p(const PartialArgs& a, hipStream_t s) {
 }
 template <class C>
 void launch_b(const BalArgs& a, hipStream_t s) {
-    decode_balanced_kernel<C><<<a.W, C::NT, 0, s>>>(a);
+    if (a.ngroups > 0) decode_balanced_kernel<C, true><<<a.W, C::NT, 0, s>>>(a);
+    else decode_balanced_kernel<C, false><<<a.W, C::NT, 0, s>>>(a);
 }
 template <class C>
 void launch_u(const UniArgs& a, hipStream_t s) {
@@ -956,14 +1006,15 @@ void launch_u(const UniArgs& a, hipStream_t s) {
 }
 template <class C>
 void launch_step(const StepArgs& a, hipStream_t s) {
-    cascade_step_kernel<C><<<a.n_dec + a.n_pre, C::NT, 0, s>>>(a);
+    if (a.d.ngroups > 0) cascade_step_kernel<C, true><<<a.n_dec + a.n_pre, C::NT, 0, s>>>(a);
+    else cascade_step_kernel<C, false><<<a.n_dec + a.n_pre, C::NT, 0, s>>>(a);
 }
 template <class C>
-int occ_step() { return occupancy_of(reinterpret_cast<const void*>(&cascade_step_kernel<C>), C::NT); }
+int occ_step() { return occupancy_of(reinterpret_cast<const void*>(&cascade_step_kernel<C, true>), C::NT); }
 template <class C>
 int occ_p() { return occupancy_of(reinterpret_cast<const void*>(&decode_partial_kernel<C>), C::NT); }
 template <class C>
-int occ_b() { return occupancy_of(reinterpret_cast<const void*>(&decode_balanced_kernel<C>), C::NT); }
+int occ_b() { return occupancy_of(reinterpret_cast<const void*>(&decode_balanced_kernel<C, true>), C::NT); }
 
 #define PD_DISPATCH(CFG, G, FN, ...)                         \
     do {                                                     \

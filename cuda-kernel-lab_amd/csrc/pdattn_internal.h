@@ -62,6 +62,10 @@ struct BalArgs {
     // row-major with this stride (row r = b * Hq + h, slot s at r * part_stride + s: the layout of
     // the reference's decode_partial, where s = chunk_base + chunk)
     int part_stride;
+    // > 0: a page-range plan of that many groups; workgroup w = g * Hkv + kvh owns the pages
+    // [nnz g / ngroups, nnz (g + 1) / ngroups) of kv_indices (its page list, in order)
+    int ngroups;
+    int nnz;
 };
 
 // The reference-shaped uniform split (decode_partial / decode_attention) run by the balanced
