@@ -34,12 +34,16 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 #include "pdattn_internal.h"
 
 namespace pdattn {
 namespace {
 
 typedef _Float16 pf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 pf16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((__vector_size__(4 * sizeof(__fp16)))) __fp16 lds_f16x4;   // the builtin's type
 typedef float pf32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t pu32x4 __attribute__((ext_vector_type(4)));
 
@@ -49,12 +53,11 @@ constexpr int kPrefixThreads = kPrefixWaves * 64;
 constexpr int kPrefixTiles = 2;                               // 16-query tiles per wave (max)
 constexpr int kPrefixRows = kPrefixWaves * kPrefixTiles * 16;  // query rows per group
 constexpr int kPrefixKB = 64;                                 // keys per LDS block
-constexpr int kPrefixVTS = 33;     // V^T row stride in dwords (32 key pairs + 1 pad)
 constexpr int kPrefixMaxPg = 512;  // pages per chunk, i.e. chunk_tokens <= 8192
 
 struct PSmem {
     pu32x4 K[2][kPrefixKB][16];              // [key][chunk ^ (key & 15)], 8 dims per chunk
-    uint32_t VT[2][kHeadDim][kPrefixVTS];    // [dim][key pair]: low half key 2p, high 2p+1
+    pu32x4 V[2][kPrefixKB][16];              // the same layout as K
     int pg[kPrefixMaxPg];                    // physical pages of this chunk
     int sq[kPrefixRows];                     // sequences of this group's rows (one per G rows)
 };
@@ -93,9 +96,8 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
                                              int kvh) {
     constexpr int PW = kPrefixWaves, PT = kPrefixThreads, QROWS = kPrefixRows, KB = kPrefixKB;
     constexpr int SR = PT / 16;             // staging rows per pass
-    constexpr int KPT = KB / SR;            // K rows per thread
-    constexpr int VPT = (KB / 2) / SR;      // V key pairs per thread
-    static_assert(KPT >= 1 && VPT >= 1 && KB % SR == 0 && (KB / 2) % SR == 0, "staging shape");
+    constexpr int KPT = KB / SR;            // K and V rows per thread
+    static_assert(KPT >= 1 && KB % SR == 0, "staging shape");
     const int G = a.Hq / a.Hkv, nq = a.ns * G;
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int l16 = lane & 15, lg = lane >> 4;
@@ -112,51 +114,36 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
     for (int i = tid; i < npg; i += PT) sm.pg[i] = a.prefix_pages[kbeg / kPage + i];
     for (int j = tid; j < nsq; j += PT) sm.sq[j] = a.seqs ? a.seqs[s0 + j] : s0 + j;
 
-    // Staging: thread t moves 16-byte chunk sc = t & 15 of K rows sr + SR i and of the V key
-    // pairs (2 p, 2 p + 1), p = sr + SR i, sr = t >> 4. Keys past the chunk read the last valid
-    // key instead (a real, finite row): their scores are masked to -inf below, so their weights
-    // are exactly 0. The loads are cached: the other query groups of the chunk, placed on the
-    // same XCD, read the same lines.
+    // Staging: thread t moves 16-byte chunk sc = t & 15 of the K and V rows sr + SR i,
+    // sr = t >> 4, into [key][chunk ^ (key & 15)]. Keys past the chunk read the last valid key
+    // instead (a real, finite row): their scores are masked to -inf below, so their weights are
+    // exactly 0. The loads are cached: the other query groups of the chunk, placed on the same
+    // XCD, read the same lines.
     const int sc = tid & 15, sr = tid >> 4;
-    pu32x4 kst[KPT], vst[2 * VPT];
+    pu32x4 kst[KPT], vst[KPT];
     // A full block (64 keys, starting on a page: kbeg is a multiple of 16) holds pages
-    // 4 kb .. 4 kb + 3 of the chunk: K row i of this thread is slot sr of page 4 kb + i, and V pair
-    // i is slots (2 sr) & 15 and +1 of page 4 kb + (2 sr) / 16 + 2 i. The in-page offsets are
-    // therefore fixed per thread; only the page ids change from block to block.
-    static_assert(KB == 4 * kPage && SR == kPage && KPT == 4 && VPT == 2, "full-block page walk");
+    // 4 kb .. 4 kb + 3 of the chunk: row i of this thread is slot sr of page 4 kb + i. The in-page
+    // offset is therefore fixed per thread; only the page ids change from block to block.
+    static_assert(KB == 4 * kPage && SR == kPage && KPT == 4, "full-block page walk");
     const uint32_t koff = (uint32_t)((sr * a.Hkv + kvh) * 256 + sc * 16);
-    const uint32_t voff = (uint32_t)((((2 * sr) & 15) * a.Hkv + kvh) * 256 + sc * 16);
-    const uint32_t vstep = (uint32_t)(a.Hkv * 256);   // the next slot of the page
-    const int vpg = (2 * sr) >> 4;
     auto gload = [&](int kb) {
         const int key0 = kbeg + kb * KB;
         if (key0 + KB <= kend) {
 #pragma unroll
             for (int i = 0; i < KPT; ++i) {
-                const size_t pid = (uint32_t)sm.pg[4 * kb + i];
-                kst[i] = *reinterpret_cast<const pu32x4*>(a.k + pid * page_bytes + koff);
-            }
-#pragma unroll
-            for (int j = 0; j < VPT; ++j) {
-                const uint8_t* vp = a.v + (size_t)(uint32_t)sm.pg[4 * kb + vpg + 2 * j] * page_bytes + voff;
-                vst[2 * j] = *reinterpret_cast<const pu32x4*>(vp);
-                vst[2 * j + 1] = *reinterpret_cast<const pu32x4*>(vp + vstep);
+                const size_t off = (size_t)(uint32_t)sm.pg[4 * kb + i] * page_bytes + koff;
+                kst[i] = *reinterpret_cast<const pu32x4*>(a.k + off);
+                vst[i] = *reinterpret_cast<const pu32x4*>(a.v + off);
             }
             return;
         }
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int key = min(key0 + sr + SR * i, kend - 1);
-            const uint32_t pid = (uint32_t)sm.pg[(key - kbeg) >> 4];
-            kst[i] = *reinterpret_cast<const pu32x4*>(
-                a.k + pid * page_bytes + (size_t)(((key & 15) * a.Hkv + kvh) * 256 + sc * 16));
-        }
-#pragma unroll
-        for (int i = 0; i < 2 * VPT; ++i) {
-            const int key = min(key0 + 2 * (sr + SR * (i >> 1)) + (i & 1), kend - 1);
-            const uint32_t pid = (uint32_t)sm.pg[(key - kbeg) >> 4];
-            vst[i] = *reinterpret_cast<const pu32x4*>(
-                a.v + pid * page_bytes + (size_t)(((key & 15) * a.Hkv + kvh) * 256 + sc * 16));
+            const size_t off = (size_t)(uint32_t)sm.pg[(key - kbeg) >> 4] * page_bytes +
+                               (size_t)(((key & 15) * a.Hkv + kvh) * 256 + sc * 16);
+            kst[i] = *reinterpret_cast<const pu32x4*>(a.k + off);
+            vst[i] = *reinterpret_cast<const pu32x4*>(a.v + off);
         }
     };
     auto lstore = [&](int buf) {
@@ -164,16 +151,7 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
         for (int i = 0; i < KPT; ++i) {
             const int n = sr + SR * i;
             sm.K[buf][n][sc ^ (n & 15)] = kst[i];
-        }
-#pragma unroll
-        for (int i = 0; i < VPT; ++i) {
-            const pu32x4 lo = vst[2 * i], hi = vst[2 * i + 1];   // keys 2 p, 2 p + 1, dims 8 sc ..
-            const int p = sr + SR * i;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                sm.VT[buf][8 * sc + 2 * e][p] = __builtin_amdgcn_perm(hi[e], lo[e], 0x05040100u);
-                sm.VT[buf][8 * sc + 2 * e + 1][p] = __builtin_amdgcn_perm(hi[e], lo[e], 0x07060302u);
-            }
+            sm.V[buf][n][sc ^ (n & 15)] = vst[i];
         }
     };
 
@@ -195,13 +173,21 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
         for (int ks = 0; ks < 4; ++ks) qb[tq][ks] = *reinterpret_cast<const pf16x8*>(qp + 32 * ks);
         qrow[tq] = ok ? b * a.Hq + kvh * G + g : -1;
     }
+    // A negative scale is moved into q: s * scale = (-s) * |scale|, and negating fp16 values
+    // (their sign bits) is exact, so the loop below only ever sees a positive scale and takes the
+    // maximum of the raw scores.
+    const float sl2 = fabsf(a.scale_log2);
+    const uint32_t qflip = a.scale_log2 < 0.f ? 0x80008000u : 0u;
 #pragma unroll
     for (int tq = 0; tq < NT; ++tq)
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-            if (qrow[tq] < 0) qb[tq][ks] = pf16x8{};
+        for (int ks = 0; ks < 4; ++ks) {
+            pu32x4 w = __builtin_bit_cast(pu32x4, qb[tq][ks]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[e] = qrow[tq] < 0 ? 0u : (w[e] ^ qflip);
+            qb[tq][ks] = __builtin_bit_cast(pf16x8, w);
+        }
 
-    const bool neg = a.scale_log2 < 0.f;   // the extremum that scales to the maximum is the minimum
     pf32x4 acc[NT][8];
     float m_run[NT], l_run[NT];
 #pragma unroll
@@ -215,7 +201,10 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
     if (nblk > 0) lstore(0);
     __syncthreads();
 
-    for (int kb = 0; kb < nblk; ++kb) {
+    // One 64-key block. Only the chunk's last block can run past its end (EDGE): its keys past the
+    // end get score -inf and weight 0, in a separate instantiation, so full blocks carry no masking.
+    auto block = [&](int kb, auto EDGE) {
+        constexpr bool edge = decltype(EDGE)::value;
         const int buf = kb & 1;
         const bool more = kb + 1 < nblk;
         if (more) gload(kb + 1);
@@ -237,44 +226,30 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
             }
         }
 
-        // Online softmax (base 2) per query. The scores stay unscaled: the maximum of the scaled
-        // scores is the scale times the maximum of the unscaled ones (the minimum for a negative
-        // scale), and each weight is exp2(fma(s, scale, -m)). Only a block that runs past the
-        // chunk's end holds masked keys: their scores are set to the value the extremum ignores
-        // (-inf, or +inf for a negative scale) and their weights to 0 below.
+        // Online softmax (base 2) per query. The scores stay unscaled: the scale is positive, so
+        // the maximum of the scaled scores is the scale times the maximum of the raw ones, and
+        // each weight is exp2(fma(s, scale, -m)).
         const int kbase = kbeg + kb * KB + 4 * lg;
-        const bool edge = kbeg + (kb + 1) * KB > kend;   // uniform over the workgroup
-        if (edge) {
-            const float ignore = neg ? INFINITY : -INFINITY;
+        if constexpr (edge) {
 #pragma unroll
             for (int tq = 0; tq < NT; ++tq)
 #pragma unroll
                 for (int tk = 0; tk < 4; ++tk)
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
-                        if (kbase + 16 * tk + j >= kend) s[tq][tk][j] = ignore;
+                        if (kbase + 16 * tk + j >= kend) s[tq][tk][j] = -INFINITY;
         }
         float mn[NT];
         bool grow = false;
 #pragma unroll
         for (int tq = 0; tq < NT; ++tq) {
-            float mx;
-            if (!neg) {
-                mx = -INFINITY;
+            float mx = -INFINITY;
 #pragma unroll
-                for (int tk = 0; tk < 4; ++tk)
+            for (int tk = 0; tk < 4; ++tk)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) mx = fmaxf(mx, s[tq][tk][j]);
-                mx = col4_reduce<true>(mx);
-            } else {
-                mx = INFINITY;
-#pragma unroll
-                for (int tk = 0; tk < 4; ++tk)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) mx = fminf(mx, s[tq][tk][j]);
-                mx = -col4_reduce<true>(-mx);
-            }
-            mn[tq] = fmaxf(m_run[tq], mx * a.scale_log2);
+                for (int j = 0; j < 4; ++j) mx = fmaxf(mx, s[tq][tk][j]);
+            mx = col4_reduce<true>(mx);
+            mn[tq] = fmaxf(m_run[tq], mx * sl2);
             grow |= mn[tq] > m_run[tq];
         }
         if (__builtin_amdgcn_ballot_w64(grow)) {
@@ -291,40 +266,40 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
 #pragma unroll
         for (int tq = 0; tq < NT; ++tq) {
             const float ms = (m_run[tq] == -INFINITY) ? 0.f : m_run[tq];
-            float pw[4][4];
-#pragma unroll
-            for (int tk = 0; tk < 4; ++tk)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) pw[tk][j] = __builtin_amdgcn_exp2f(fmaf(s[tq][tk][j], a.scale_log2, -ms));
-            if (edge) {   // masked keys weigh 0 whatever the scale (0 * inf would not)
-#pragma unroll
-                for (int tk = 0; tk < 4; ++tk)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        if (kbase + 16 * tk + j >= kend) pw[tk][j] = 0.f;
-            }
 #pragma unroll
             for (int tk = 0; tk < 4; ++tk)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    l_run[tq] += pw[tk][j];   // fp32 weights for the denominator (exact lse); PV
-                    pb[tq][tk >> 1][(tk & 1) * 4 + j] = (_Float16)pw[tk][j];   // uses them rounded to nearest
+                    float p = __builtin_amdgcn_exp2f(fmaf(s[tq][tk][j], sl2, -ms));
+                    if constexpr (edge)   // masked keys weigh 0 whatever the scale (0 * inf would not)
+                        if (kbase + 16 * tk + j >= kend) p = 0.f;
+                    l_run[tq] += p;   // fp32 weights for the denominator (exact lse); PV uses
+                    pb[tq][tk >> 1][(tk & 1) * 4 + j] = (_Float16)p;   // them rounded to nearest
                 }
         }
 
-        // O^T += V^T P^T
+        // O^T += V^T P^T. The A operand (dims 16 dt + l16, keys of k-elements 4 h .. 4 h + 3 =
+        // keys 32 kb2 + 16 h + 4 lg + 0..3, the order of P's) comes from the row-major V tile by
+        // transposing reads: within a 16-lane group, lane j reads 4 dims (16 dt + 4 (j & 3) ..)
+        // of key 32 kb2 + 16 h + 4 lg + (j >> 2), and lane i receives element (i & 3) of lanes
+        // i / 4, i / 4 + 4, ..., i.e. dim 16 dt + i of the 4 keys.
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
-            const int d = 16 * dt + l16;
 #pragma unroll
             for (int kb2 = 0; kb2 < 2; ++kb2) {
-                const int p0 = 16 * kb2 + 2 * lg;
-                pu32x4 raw;
-                raw[0] = sm.VT[buf][d][p0];
-                raw[1] = sm.VT[buf][d][p0 + 1];
-                raw[2] = sm.VT[buf][d][p0 + 8];
-                raw[3] = sm.VT[buf][d][p0 + 9];
-                const pf16x8 va = __builtin_bit_cast(pf16x8, raw);
+                pf16x4 half[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int key = 32 * kb2 + 16 * h + 4 * lg + (l16 >> 2);
+                    const int chunk = 2 * dt + ((l16 & 3) >> 1);
+                    const _Float16* src = reinterpret_cast<const _Float16*>(&sm.V[buf][key][chunk ^ (key & 15)]) +
+                                          4 * (l16 & 1);
+                    half[h] = __builtin_bit_cast(pf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                        (__attribute__((address_space(3))) lds_f16x4*)(
+                            (__attribute__((address_space(3))) _Float16*)src)));
+                }
+                const pf16x8 va = {half[0][0], half[0][1], half[0][2], half[0][3],
+                                   half[1][0], half[1][1], half[1][2], half[1][3]};
 #pragma unroll
                 for (int tq = 0; tq < NT; ++tq) acc[tq][dt] = mfma16x16x32(va, pb[tq][kb2], acc[tq][dt]);
             }
@@ -332,7 +307,10 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
 
         if (more) lstore(buf ^ 1);
         __syncthreads();
-    }
+    };
+    const int nfull = nkeys / KB;
+    for (int kb = 0; kb < nfull; ++kb) block(kb, std::false_type{});
+    if (nfull < nblk) block(nfull, std::true_type{});
 
     // normalized partial of this chunk
 #pragma unroll
