@@ -15,19 +15,20 @@
 //     tile is an in-lane max plus two VALU lane swaps (col4_reduce), and the rescale of the output
 //     accumulator by exp(m_old - m_new) is a per-lane scalar multiply;
 //   * P leaves the S^T accumulator already in the B-operand layout of the PV product (the 8
-//     keys a lane contributes are 4 of one 16-key tile and 4 of the next; V^T is read with the
-//     same key order), so P needs no cross-lane movement.
-// K is staged in LDS as [key][16-byte chunk] with the chunk index XOR-ed by (key & 15): the
-// A-operand reads (16 keys x one chunk per 16-lane phase) hit 16 distinct bank groups. V is
-// staged transposed (V^T[dim][key pair], rows padded to 33 dwords) so that the A operand of the
-// PV product is two conflict-free 8-byte reads. Two LDS buffers: the global loads of block n+1
-// are in flight while block n is computed.
+//     keys a lane contributes are 4 of one 16-key tile and 4 of the next), so P needs no
+//     cross-lane movement.
+// K and V are staged in LDS row-major, [key][16-byte chunk], with the chunk index XOR-ed by a
+// function of the key: the K A-operand reads (16 keys x one chunk per 16-lane phase) and the V
+// reads below each hit every LDS bank once. The A operand of the PV product (V^T: 16 dims x 8
+// keys per lane, in P's key order) comes from gfx950's transposing LDS read (ds_read_b64_tr_b16),
+// two per MFMA, so V needs no transpose pass. Two LDS buffers: the global loads of block n+1 are
+// in flight while block n is computed.
 //
 // A workgroup: 4 waves x 2 query tiles x 16 = 128 stacked query rows of one kv head, one chunk
 // of prefix keys, written as the normalized partial (o, lse) of that chunk. The query rows are
 // those of the sequences that share the prefix (all B, or a listed subset for one node of a
 // prefix tree); chunk c of the prefix writes partial column col0 + c of each of their rows. About
-// 210 VGPRs per wave and 69 KB of LDS: two such workgroups share a CU (two waves per SIMD), or one
+// 240 VGPRs per wave and 67 KB of LDS: two such workgroups share a CU (two waves per SIMD), or one
 // shares it with a decode workgroup of the fused cascade step, and the accumulators stay out of
 // AGPRs, so the softmax rescale touches them in place.
 #pragma once
@@ -57,7 +58,7 @@ constexpr int kPrefixMaxPg = 512;  // pages per chunk, i.e. chunk_tokens <= 8192
 
 struct PSmem {
     pu32x4 K[2][kPrefixKB][16];              // [key][chunk ^ (key & 15)], 8 dims per chunk
-    pu32x4 V[2][kPrefixKB][16];              // the same layout as K
+    pu32x4 V[2][kPrefixKB][16];              // [key][chunk ^ ((key & 7) << 1)]
     int pg[kPrefixMaxPg];                    // physical pages of this chunk
     int sq[kPrefixRows];                     // sequences of this group's rows (one per G rows)
 };
@@ -115,7 +116,9 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
     for (int j = tid; j < nsq; j += PT) sm.sq[j] = a.seqs ? a.seqs[s0 + j] : s0 + j;
 
     // Staging: thread t moves 16-byte chunk sc = t & 15 of the K and V rows sr + SR i,
-    // sr = t >> 4, into [key][chunk ^ (key & 15)]. Keys past the chunk read the last valid key
+    // sr = t >> 4, into [key][chunk ^ (key & 15)] (K) and [key][chunk ^ ((key & 7) << 1)] (V: the
+    // swizzle under which each half-wave of the transposing reads below, 8 keys x 2 chunks x 2
+    // halves, covers every LDS bank once). Keys past the chunk read the last valid key
     // instead (a real, finite row): their scores are masked to -inf below, so their weights are
     // exactly 0. The loads are cached: the other query groups of the chunk, placed on the same
     // XCD, read the same lines.
@@ -151,7 +154,7 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
         for (int i = 0; i < KPT; ++i) {
             const int n = sr + SR * i;
             sm.K[buf][n][sc ^ (n & 15)] = kst[i];
-            sm.V[buf][n][sc ^ (n & 15)] = vst[i];
+            sm.V[buf][n][sc ^ ((n & 7) << 1)] = vst[i];
         }
     };
 
@@ -292,8 +295,8 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
                 for (int h = 0; h < 2; ++h) {
                     const int key = 32 * kb2 + 16 * h + 4 * lg + (l16 >> 2);
                     const int chunk = 2 * dt + ((l16 & 3) >> 1);
-                    const _Float16* src = reinterpret_cast<const _Float16*>(&sm.V[buf][key][chunk ^ (key & 15)]) +
-                                          4 * (l16 & 1);
+                    const _Float16* src =
+                        reinterpret_cast<const _Float16*>(&sm.V[buf][key][chunk ^ ((key & 7) << 1)]) + 4 * (l16 & 1);
                     half[h] = __builtin_bit_cast(pf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
                         (__attribute__((address_space(3))) lds_f16x4*)(
                             (__attribute__((address_space(3))) _Float16*)src)));
