@@ -5,6 +5,8 @@
   null), and calls would also cost registers and latency in the hot loop.
 * No packed-FP32 instructions are emitted (the build disables them).
 * No kernel spills registers to scratch.
+
+Every .hip source of the library is checked.
 """
 import os
 import re
@@ -26,8 +28,15 @@ def _asm(name, tmp_path):
     return out.read_text()
 
 
+SOURCES = sorted(f[:-4] for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+
+def test_every_source_is_linted():
+    assert {"decode", "cascade", "append", "misc", "noalloc"} <= set(SOURCES)
+
+
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
-@pytest.mark.parametrize("name", ["decode", "cascade", "misc"])
+@pytest.mark.parametrize("name", SOURCES)
 def test_no_calls_no_packed_fp32(name, tmp_path):
     asm = _asm(name, tmp_path)
     assert "s_swappc_b64" not in asm, f"{name}.hip: a kernel calls a device function"
@@ -35,12 +44,16 @@ def test_no_calls_no_packed_fp32(name, tmp_path):
 
 
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
-def test_no_scratch_spills(tmp_path):
-    out = subprocess.run([HIPCC, *FLAGS, "-c", os.path.join(CSRC, "decode.hip"), "-o", str(tmp_path / "d.o"),
+@pytest.mark.parametrize("name", SOURCES)
+def test_no_scratch_spills(name, tmp_path):
+    out = subprocess.run([HIPCC, *FLAGS, "-c", os.path.join(CSRC, name + ".hip"), "-o", str(tmp_path / "d.o"),
                           "-Rpass-analysis=kernel-resource-usage"], capture_output=True, text=True)
     text = out.stderr
     names = re.findall(r"Function Name: (\S+)", text)
     spills = re.findall(r"VGPRs Spill: (\d+)", text)
-    assert names and len(names) == len(spills)
-    for n, sp in zip(names, spills):
-        assert int(sp) == 0, f"{n} spills {sp} VGPRs"
+    sspills = re.findall(r"SGPRs Spill: (\d+)", text)
+    assert len(names) == len(spills) == len(sspills)
+    if name != "noalloc":   # (noalloc.hip holds a device array and host code, no kernel)
+        assert names
+    for n, sp, ss in zip(names, spills, sspills):
+        assert int(sp) == 0 and int(ss) == 0, f"{name}.hip: {n} spills {sp} VGPRs, {ss} SGPRs"
