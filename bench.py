@@ -44,6 +44,9 @@ def parse():
                     help="run one workload only (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only torch copies of COPY_BYTES (known-size traffic for counter runs)")
+    ap.add_argument("--timeline", default="", choices=["", "32k", "64x1k", "prefix", "cascade"],
+                    help="per-workgroup phase timestamps from the timeline build of the library "
+                         "(make -C cuda-kernel-lab_amd timeline) instead of the bench")
     return ap.parse_args()
 
 
@@ -600,6 +603,142 @@ def tree_workload(timer, args):
             "tree_levels": info.levels}
 
 
+TIMELINE_LIB = os.path.join(ROOT, "cuda-kernel-lab_amd", "lib", "timeline", "libpdattn.so")
+TL_ROWS, TL_SLOTS = 8192, 32          # the stamp table of csrc/timeline.h
+DECODE_STAMPS = ([(0, "start"), (1, "descriptors staged"), (2, "q rows staged"), (3, "first ring step")]
+                 + [(4 + 2 * s, f"segment {s} streamed") for s in range(12)]
+                 + [(5 + 2 * s, f"segment {s} flushed") for s in range(12)] + [(31, "done")])
+PREFIX_STAMPS = ([(0, "start"), (1, "ids staged"), (2, "block 0 in LDS")]
+                 + [(3 + k, f"block {k} done") for k in range(24)]
+                 + [(29, "blocks done"), (30, "partials written")])
+
+
+def timeline(args):
+    """Phase timestamps of every workgroup (thread 0's s_memrealtime at the stamps of
+    csrc/timeline.h), in µs from the launch's first workgroup start: for each stamp the median
+    over workgroups and the last workgroup, medians over `reps` launches. "cold": a 1 GiB flush
+    before the launch; "b2b": the last of a run of launches back to back (the decode cases over
+    rotated K/V copies of >= 1 GiB, so every launch reads from HBM)."""
+    import ctypes
+    import numpy as np
+    import torch
+    import pdattn
+    if not os.path.exists(TIMELINE_LIB):
+        sys.exit("no timeline build: run make -C cuda-kernel-lab_amd timeline")
+    pdattn._lib = None
+    pdattn.LIB_PATH = TIMELINE_LIB
+    L = pdattn.lib()
+    for t in ("decode", "prefix"):
+        getattr(L, "pdattn_timeline_read_" + t).argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    timer = Timer()
+    s = timer.stream
+    reps = max(3, min(args.steps, 9))
+
+    def grab(table):
+        torch.cuda.synchronize()
+        buf = np.zeros(TL_ROWS * TL_SLOTS, np.uint64)
+        assert getattr(L, "pdattn_timeline_read_" + table)(buf.ctypes.data, buf.nbytes) == 0
+        return buf.reshape(TL_ROWS, TL_SLOTS).astype(np.int64)
+
+    def reset(table):
+        assert getattr(L, "pdattn_timeline_reset_" + table)() == 0
+
+    def summary(runs, lo, hi, stamps):
+        """runs: tables of the launches; rows [lo, hi) are the workgroups of one role."""
+        rel = []
+        for a in runs:
+            a = a[lo:hi]
+            t0 = a[:, 0][a[:, 0] > 0].min()
+            rel.append(np.where(a > 0, (a - t0) * 0.01, np.nan))   # 100 MHz counter
+        out = {}
+        for slot, name in stamps:
+            col = np.stack([r[:, slot] for r in rel])
+            if np.isnan(col).all():
+                continue
+            med = np.nanmedian([np.nanmedian(c) for c in col])
+            last = np.nanmedian([np.nanmax(c) for c in col])
+            out[name] = [round(float(med), 2), round(float(last), 2)]
+        return out
+
+    def report(case, mode, workgroups, stamps):
+        print(json.dumps({"timeline": case, "mode": mode, "workgroups": workgroups,
+                          "stamps_us_median_last": stamps}), flush=True)
+
+    if args.timeline in ("32k", "64x1k"):
+        lens = [32768] if args.timeline == "32k" else [1024] * 64
+        bt, t = make_device_batch(lens, 32, 8, seed=11)
+        fn, plan, ws = streamk_runner(bt, t, s)
+        W = plan.info().workgroups
+        reset("decode")
+        runs = []
+        for _ in range(reps):
+            fn()
+            reset("decode")
+            timer.flush()
+            fn()
+            runs.append(grab("decode"))
+        report(args.timeline, "cold", W, summary(runs, 0, W, DECODE_STAMPS))
+        kv_bytes = 2 * t["k"].numel() * t["k"].element_size()
+        n = max(2, -(-ROT_BYTES // kv_bytes))
+        ks = [t["k"]] + [torch.empty_like(t["k"]).normal_() for _ in range(n - 1)]
+        vs = [t["v"]] + [torch.empty_like(t["v"]).normal_() for _ in range(n - 1)]
+        runs = []
+        for _ in range(reps):
+            for i in range(2 * n):
+                plan.run(t["q"], ks[i % n], vs[i % n], t["indptr"], t["indices"], t["last"], t["out"],
+                         t["lse"], ws, ws.numel(), stream=s)
+            runs.append(grab("decode"))
+        report(args.timeline, "b2b", W, summary(runs, 0, W, DECODE_STAMPS))
+        return
+    if args.timeline == "prefix":
+        bt, t = make_device_batch(None, 32, 8, seed=21, shared_prefix=8192, suffix=[512] * 64)
+        for ct in (512, 256):
+            nch = 8192 // ct
+            po = torch.empty(bt.B * 32, nch, 128, dtype=torch.float32, device="cuda:0")
+            pl = torch.empty(bt.B * 32, nch, dtype=torch.float32, device="cuda:0")
+            pp = pdattn.PrefixParams()
+            pp.q, pp.k_cache, pp.v_cache = t["q"].data_ptr(), t["k"].data_ptr(), t["v"].data_ptr()
+            pp.prefix_pages = t["indices"].data_ptr()
+            pp.part_o, pp.part_lse = po.data_ptr(), pl.data_ptr()
+            pp.B, pp.Hq, pp.Hkv = bt.B, 32, 8
+            pp.prefix_len, pp.chunk_tokens, pp.part_stride = 8192, ct, nch
+            pp.sm_scale = float(1.0 / np.sqrt(128))
+            W = nch * 2 * 8
+            reset("prefix")   # (the other chunk size stamps other slots)
+            runs = []
+            for _ in range(reps):
+                for _ in range(4):
+                    pdattn.cascade_prefix(pp, s)
+                runs.append(grab("prefix"))
+            report(f"prefix 64x8192, {ct}-token chunks", "b2b", W, summary(runs, 0, W, PREFIX_STAMPS))
+        return
+    # the fused cascade step at config 5: decode-role and prefix-role workgroups
+    bt, t = make_device_batch(None, 32, 8, seed=21, shared_prefix=8192, suffix=[512] * 64)
+    base = pdattn.make_params(t["q"], t["k"], t["v"], t["indptr"], t["indices"], t["last"], bt.B, 32, 8)
+    cp = pdattn.CascadePlan(base, bt.indptr, bt.indices, bt.lens, t["indices"])
+    cws = pdattn.Workspace()
+    info = cp.info()
+    nd, npre = info.suffix_workgroups, info.prefix_workgroups
+    for mode in ("cold", "b2b"):
+        reset("decode")
+        runs = []
+        for _ in range(reps):
+            cp.decode(t["out"], t["lse"], cws, s)
+            if mode == "cold":
+                reset("decode")
+                timer.flush()
+                cp.decode(t["out"], t["lse"], cws, s)
+            else:
+                for _ in range(4):
+                    cp.decode(t["out"], t["lse"], cws, s)
+            runs.append(grab("decode"))
+        report("cascade 64x(8192+512) step, decode role", mode, nd, summary(runs, 0, nd, DECODE_STAMPS))
+        report("cascade 64x(8192+512) step, prefix role", mode, npre,
+               summary(runs, nd, nd + npre, PREFIX_STAMPS))
+    cp.close()
+    pdattn.workspace_release(cws)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -607,6 +746,9 @@ def main():
               f"(one GPU per box; the path would shard by sequence / kv head with no exchange)",
               file=sys.stderr)
         sys.exit(2)
+    if args.timeline:
+        timeline(args)
+        return
     import torch
     import pdattn
     pdattn.lib()

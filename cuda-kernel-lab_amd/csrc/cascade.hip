@@ -1,5 +1,9 @@
 // cascade.hip -- the prefix kernel of the shared-prefix (cascade) path: one workgroup per
 // (prefix chunk or tree item, query group, kv head), the body in prefix_body.h.
+#include "timeline.h"
+
+PD_TIMELINE_TABLE(prefix)
+
 #include "prefix_body.h"
 
 namespace pdattn {

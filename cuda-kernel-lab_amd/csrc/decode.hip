@@ -40,6 +40,10 @@
 #include <cstdlib>
 
 #include "pdattn_internal.h"
+#include "timeline.h"
+
+PD_TIMELINE_TABLE(decode)
+
 #include "prefix_body.h"
 
 namespace pdattn {
@@ -734,6 +738,10 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
     // descriptor block: a header of 8 ints, then the segments.
     int* seg = sd + 8;
     auto fld = [&](int si, int f) { return __builtin_amdgcn_readfirstlane(seg[si * kSegInts + f]); };
+    // timestamps (timeline build only): 0 start, 1 descriptors (and page ids) staged, 2 q rows
+    // staged, 3 the first ring step computed, 4 + 2 s / 5 + 2 s segment s streamed / flushed
+    // (s < 12), 31 done; thread 0 of the workgroup
+    PD_STAMP(0);
     constexpr int PMAX = kRangeMax / NT, QPS = G * kHeadDim / 8;
     constexpr int QMAX = (BalShared<C, COMPACT>::SEGS * QPS + NT - 1) / NT;
     // A page-range plan (RANGES: ngroups > 0) gives workgroup w = g * Hkv + kvh the pages
@@ -765,6 +773,7 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
         for (int k = 0; k < PMAX; ++k)
             if (tid + k * NT < npr) pg[tid + k * NT] = pv[k];
         __syncthreads();
+        PD_STAMP(1);
         nseg = __builtin_amdgcn_readfirstlane(sd[0]);
         if (nseg <= 0) return;   // uniform: every thread leaves
     } else {
@@ -801,6 +810,7 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
             seg[tid * kSegInts + 2] = qa;
         }
         __syncthreads();
+        PD_STAMP(1);
     }
 
     const uint32_t page_bytes = (uint32_t)(kPage * a.Hkv * 256);
@@ -893,6 +903,7 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
         }
     }
     __syncthreads();
+    PD_STAMP(2);
     if constexpr (!RANGES) {
         seek();
 #pragma unroll
@@ -922,12 +933,16 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
                     page_step<C>(st, buf[u], qv, tbase + (wave + NW * (blk + u)) * kPage, r, t0, t1,
                                  a.scale_log2);
             }
+            if (si == 0 && blk == 0) PD_STAMP(3);
         }
+        if (si < 12) PD_STAMP(4 + 2 * si);
         flush_segment<C, BalShared<C, COMPACT>::HP>(sm, st, kargs(),
                                                     (size_t)fld(si, 0) * a.Hq + (size_t)fld(si, 1) * G,
                                                     fld(si, 7));
         reset_state<C>(st);
+        if (si < 12) PD_STAMP(5 + 2 * si);
     }
+    PD_STAMP(31);
 }
 
 // At G = 8 the per-page VALU work is about twice G = 4's and no longer hides under the page's

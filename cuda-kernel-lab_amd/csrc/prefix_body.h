@@ -38,6 +38,7 @@
 #include <type_traits>
 
 #include "pdattn_internal.h"
+#include "timeline.h"
 
 namespace pdattn {
 namespace {
@@ -111,6 +112,9 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
     const int s0 = qgrp * (QROWS / G);                 // first member of this query group
     const int nsq = min(QROWS / G, a.ns - s0);
 
+    // timestamps (timeline build only): 0 start, 1 page and member ids staged, 2 the first key
+    // block in LDS, 3 + k key block k done (k < 24), 29 all blocks done, 30 partials written
+    PD_STAMP(0);
     // page ids and member ids in one round trip
     for (int i = tid; i < npg; i += PT) sm.pg[i] = a.prefix_pages[kbeg / kPage + i];
     for (int j = tid; j < nsq; j += PT) sm.sq[j] = a.seqs ? a.seqs[s0 + j] : s0 + j;
@@ -159,6 +163,7 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
     };
 
     __syncthreads();   // page ids, member ids
+    PD_STAMP(1);
     if (nblk > 0) gload(0);
 
     // B operands of S^T: Q[query][32 ks + 8 lg .. +7], query = l16 of tile tq; loaded behind the
@@ -203,6 +208,7 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
 
     if (nblk > 0) lstore(0);
     __syncthreads();
+    PD_STAMP(2);
 
     // One 64-key block. Only the chunk's last block can run past its end (EDGE): its keys past the
     // end get score -inf and weight 0, in a separate instantiation, so full blocks carry no masking.
@@ -310,11 +316,13 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
 
         if (more) lstore(buf ^ 1);
         __syncthreads();
+        if (kb < 24) PD_STAMP(3 + kb);
     };
     const int nfull = nkeys / KB;
     for (int kb = 0; kb < nfull; ++kb) block(kb, std::false_type{});
     if (nfull < nblk) block(nfull, std::true_type{});
 
+    PD_STAMP(29);
     // normalized partial of this chunk
 #pragma unroll
     for (int tq = 0; tq < NT; ++tq) {
@@ -328,6 +336,7 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
         if (lg == 0)
             a.part_lse[slot] = L > 0.f ? (m_run[tq] + __builtin_amdgcn_logf(L)) * kPrefixLn2 : -INFINITY;
     }
+    PD_STAMP(30);
 }
 
 // One prefix workgroup: item x of a multi-prefix launch ({page-table position of the node's
