@@ -115,7 +115,7 @@ class Timer:
         return times
 
 
-def streamk_runner(bt, t, stream):
+def plan_runner(bt, t, stream):
     import torch
     import pdattn
     plan = pdattn.Plan(bt.indptr, bt.last, bt.B, bt.Hq, bt.Hkv)
@@ -285,7 +285,7 @@ def decode_workload(timer, lens, args, with_uniform, seed=11, nosplit=False):
     import torch
     s = timer.stream
     bt, t = make_device_batch(lens, 32, 8, seed=seed)
-    fn_sk, plan, ws = streamk_runner(bt, t, s)
+    fn_sk, plan, ws = plan_runner(bt, t, s)
     fns, keep = [fn_sk], []
     if with_uniform:
         fn_un, k_un, nc = uniform_runner(bt, t, s)
@@ -357,7 +357,7 @@ def cascade_shape_leg(timer, args, B, Lp, Ls):
     from pdattn import inputs
     s = timer.stream
     bt, t = make_device_batch(None, 32, 8, seed=21, shared_prefix=Lp, suffix=[Ls] * B)
-    f_plan, plan, ws = streamk_runner(bt, t, s)
+    f_plan, plan, ws = plan_runner(bt, t, s)
     f_uni, keep, nc = uniform_runner(bt, t, s)
     base = pdattn.make_params(t["q"], t["k"], t["v"], t["indptr"], t["indices"], t["last"], bt.B, 32, 8)
     cp = pdattn.CascadePlan(base, bt.indptr, bt.indices, bt.lens, t["indices"])
@@ -391,7 +391,7 @@ def cascade_workload(timer, args, Hq=32, Hkv=8):
     import pdattn
     s = timer.stream
     bt3, t3 = make_device_batch(None, Hq, Hkv, seed=21, shared_prefix=8192, suffix=[512] * 64)
-    f3n, plan3, ws3 = streamk_runner(bt3, t3, s)
+    f3n, plan3, ws3 = plan_runner(bt3, t3, s)
     base = pdattn.make_params(t3["q"], t3["k"], t3["v"], t3["indptr"], t3["indices"], t3["last"],
                               bt3.B, Hq, Hkv)
     cp = pdattn.CascadePlan(base, bt3.indptr, bt3.indices, bt3.lens, t3["indices"])
@@ -508,7 +508,7 @@ def graph_workload(timer, args):
     s = timer.stream
     out = {}
     bt, t = make_device_batch([32768], 32, 8, seed=11)
-    fn, plan, ws = streamk_runner(bt, t, s)
+    fn, plan, ws = plan_runner(bt, t, s)
     fn()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
@@ -546,7 +546,7 @@ def op_workload(timer, args):
     import pdattn.torch_ops  # noqa: F401
     s = timer.stream
     bt, t = make_device_batch([32768], 32, 8, seed=11)
-    fn, plan, ws = streamk_runner(bt, t, s)
+    fn, plan, ws = plan_runner(bt, t, s)
     iph = torch.from_numpy(bt.indptr.astype("int32"))
     lah = torch.from_numpy(bt.last.astype("int32"))
     sc = float(1.0 / 128 ** 0.5)
@@ -579,7 +579,7 @@ def tree_workload(timer, args):
              last=torch.from_numpy(bt.last).to(d),
              out=torch.empty(bt.B, 32, 128, dtype=torch.float16, device=d),
              lse=torch.empty(bt.B, 32, dtype=torch.float32, device=d))
-    fn, plan, ws = streamk_runner(bt, t, s)
+    fn, plan, ws = plan_runner(bt, t, s)
     base = pdattn.make_params(t["q"], t["k"], t["v"], t["indptr"], t["indices"], t["last"], bt.B, 32, 8)
     plans, fns = [], [fn]
     for tree in (False, True):
@@ -667,7 +667,7 @@ def timeline(args):
     if args.timeline in ("32k", "64x1k"):
         lens = [32768] if args.timeline == "32k" else [1024] * 64
         bt, t = make_device_batch(lens, 32, 8, seed=11)
-        fn, plan, ws = streamk_runner(bt, t, s)
+        fn, plan, ws = plan_runner(bt, t, s)
         W = plan.info().workgroups
         reset("decode")
         runs = []

@@ -62,7 +62,7 @@ def run_uniform(db: DeviceBatch, force_chunks: int = 0):
     return o, l, nc
 
 
-def run_streamk(db: DeviceBatch, force_workgroups: int = 0):
+def run_plan(db: DeviceBatch, force_workgroups: int = 0):
     bt = db.bt
     plan = pdattn.Plan(bt.indptr, bt.last, bt.B, bt.Hq, bt.Hkv, force_workgroups)
     ws = torch.empty(max(plan.workspace_bytes, 256), dtype=torch.uint8, device=device())

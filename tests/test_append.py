@@ -162,10 +162,10 @@ def test_append_prefill_many_tokens_per_workgroup(Hkv, lens):
 @pytest.mark.gpu
 def test_decode_after_append_matches_oracle():
     from _checks import check_lse, check_out
-    from _gpu import run_streamk
+    from _gpu import run_plan
     lens = [129, 1000, 16, 2049]
     bt, db, kc, vc = _gpu_append_case(lens, 32, 8, np.arange(4), np.array(lens) - 1, seed=9)
-    o, l, _ = run_streamk(db)
+    o, l, _ = run_plan(db)
     ro, rl = oracle.decode(bt.q, kc, vc, bt.indptr, bt.indices, bt.last, 32, 8)
     check_out(o, ro, tag="decode after append")
     check_lse(l, rl, tag="decode after append")

@@ -54,9 +54,9 @@ def test_cascade_benchmark_config():
     assert info.use == 1 and info.prefix_tokens == 8192
     check_out(o, ro, tag="cascade")
     check_lse(l, rl, tag="cascade")
-    o2, l2, _ = _gpu.run_streamk(db)
-    check_out(o2, ro, tag="non-shared stream-K")
-    check_lse(l2, rl, tag="non-shared stream-K")
+    o2, l2, _ = _gpu.run_plan(db)
+    check_out(o2, ro, tag="non-shared plan")
+    check_lse(l2, rl, tag="non-shared plan")
 
 
 @pytest.mark.parametrize("chunk_tokens", [16, 64, 96, 1024])

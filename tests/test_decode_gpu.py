@@ -51,10 +51,10 @@ def test_uniform_split_matches_oracle(ref_case, force):
 
 
 @pytest.mark.parametrize("wg", [0, 1, 3, 7, 64, 1000])
-def test_streamk_matches_oracle(ref_case, wg):
+def test_plan_matches_oracle(ref_case, wg):
     import _gpu
     bt, db, ro, rl = ref_case
-    o, l, info = _gpu.run_streamk(db, wg)
+    o, l, info = _gpu.run_plan(db, wg)
     check_out(o, ro, tag=f"W={info.workgroups}")
     check_lse(l, rl, tag=f"W={info.workgroups}")
 
@@ -203,9 +203,9 @@ def test_baseline_configs_match_oracle(cfg):
     bt = inputs.make_batch(lens, 32, 8, seed=seed)
     ro, rl = _ref(bt)
     db = _gpu.DeviceBatch(bt)
-    o, l, info = _gpu.run_streamk(db)
-    check_out(o, ro, tag=f"{tag} stream-K W={info.workgroups}")
-    check_lse(l, rl, tag=f"{tag} stream-K")
+    o, l, info = _gpu.run_plan(db)
+    check_out(o, ro, tag=f"{tag} plan W={info.workgroups}")
+    check_lse(l, rl, tag=f"{tag} plan")
     o, l, nc = _gpu.run_uniform(db)
     check_out(o, ro, tag=f"{tag} uniform chunks={nc}")
     check_lse(l, rl, tag=f"{tag} uniform")
@@ -218,22 +218,22 @@ def test_empty_sequences(lens):
     ro, rl = _ref(bt)
     db = _gpu.DeviceBatch(bt)
     for wg in (0, 1, 5):
-        o, l, _ = _gpu.run_streamk(db, wg)
-        check_out(o, ro, tag=f"stream-K W={wg}")
-        check_lse(l, rl, tag=f"stream-K W={wg}")
+        o, l, _ = _gpu.run_plan(db, wg)
+        check_out(o, ro, tag=f"plan W={wg}")
+        check_lse(l, rl, tag=f"plan W={wg}")
     o, l, _ = _gpu.run_uniform(db)
     check_out(o, ro, tag="uniform")
     check_lse(l, rl, tag="uniform")
 
 
-def test_streamk_bitwise_deterministic():
+def test_plan_bitwise_deterministic():
     """Split pairs are merged in fixed order, whoever arrives last."""
     import _gpu
     bt = inputs.make_batch([5000, 3001, 17], 32, 8, seed=2)
     db = _gpu.DeviceBatch(bt)
     first = None
     for _ in range(5):
-        o, l, info = _gpu.run_streamk(db, 97)
+        o, l, info = _gpu.run_plan(db, 97)
         assert info.split_pairs > 0
         if first is None:
             first = (o.copy(), l.copy())
@@ -242,7 +242,7 @@ def test_streamk_bitwise_deterministic():
 
 
 @pytest.mark.parametrize("Hq,Hkv", [(8, 8), (16, 8), (32, 8), (32, 4)], ids=["G1", "G2", "G4", "G8"])
-@pytest.mark.parametrize("path", ["streamk", "uniform"])
+@pytest.mark.parametrize("path", ["plan", "uniform"])
 def test_bitwise_deterministic_every_group_size(Hq, Hkv, path):
     """Each kernel instantiation (G = 1, 2, 4, 8; balanced and uniform-split paths) gives the
     same bits on repeated launches, with split pairs merged."""
@@ -252,8 +252,8 @@ def test_bitwise_deterministic_every_group_size(Hq, Hkv, path):
     db = _gpu.DeviceBatch(bt)
     first = None
     for _ in range(4):
-        if path == "streamk":
-            o, l, info = _gpu.run_streamk(db, 61)
+        if path == "plan":
+            o, l, info = _gpu.run_plan(db, 61)
             assert info.split_pairs > 0
         else:
             o, l, nc = _gpu.run_uniform(db, 5)
@@ -282,9 +282,9 @@ def test_random_batches_match_oracle(seed):
     bt = inputs.make_batch(lens, G * Hkv, Hkv, seed=seed)
     db = _gpu.DeviceBatch(bt)
     ro, rl = _ref(bt)
-    o, l, info = _gpu.run_streamk(db, wg)
-    check_out(o, ro, tag=f"random stream-K seed={seed} W={info.workgroups}")
-    check_lse(l, rl, tag=f"random stream-K seed={seed}")
+    o, l, info = _gpu.run_plan(db, wg)
+    check_out(o, ro, tag=f"random plan seed={seed} W={info.workgroups}")
+    check_lse(l, rl, tag=f"random plan seed={seed}")
     force = int(rng.integers(0, 9))
     o, l, nc = _gpu.run_uniform(db, force)
     check_out(o, ro, tag=f"random uniform seed={seed} chunks={nc}")
@@ -296,7 +296,7 @@ def test_page_permutation_invariance():
     import _gpu
     bt = inputs.make_batch([700, 1500], 16, 4, seed=4)
     db = _gpu.DeviceBatch(bt)
-    o1, l1, _ = _gpu.run_streamk(db, 13)
+    o1, l1, _ = _gpu.run_plan(db, 13)
     rng = np.random.default_rng(1)
     perm = rng.permutation(bt.num_pages)          # new slot of physical page i
     k2 = np.empty_like(bt.k)
@@ -305,16 +305,16 @@ def test_page_permutation_invariance():
     v2[perm] = bt.v
     bt2 = inputs.Batch(bt.lens, bt.Hq, bt.Hkv, bt.indptr, perm[bt.indices].astype(np.int32),
                        bt.last, bt.num_pages, bt.seed, bt.q, k2, v2)
-    o2, l2, _ = _gpu.run_streamk(_gpu.DeviceBatch(bt2), 13)
+    o2, l2, _ = _gpu.run_plan(_gpu.DeviceBatch(bt2), 13)
     assert np.array_equal(o1, o2) and np.array_equal(l1, l2)
 
 
 def test_split_invariance_across_workgroup_counts():
-    """Different stream-K cuts agree within fp32 rounding of the merge."""
+    """Different plan cuts agree within fp32 rounding of the merge."""
     import _gpu
     bt = inputs.make_batch([4096, 2500, 100], 32, 8, seed=6)
     db = _gpu.DeviceBatch(bt)
-    outs = [_gpu.run_streamk(db, wg)[:2] for wg in (1, 24, 256, 2000)]
+    outs = [_gpu.run_plan(db, wg)[:2] for wg in (1, 24, 256, 2000)]
     for o, l in outs[1:]:
         assert np.max(np.abs(o - outs[0][0])) <= 2e-3
         assert np.max(np.abs(l - outs[0][1])) <= 1e-4

@@ -45,9 +45,9 @@ def test_library_matches_fixture(path):
     bt, z = load(path)
     db = _gpu.DeviceBatch(bt)
     for wg in (0, 1, 5):
-        o, l, _ = _gpu.run_streamk(db, wg)
-        check_out(o, z["out"], tag=f"stream-K W={wg}")
-        check_lse(l, z["lse"], tag=f"stream-K W={wg}")
+        o, l, _ = _gpu.run_plan(db, wg)
+        check_out(o, z["out"], tag=f"plan W={wg}")
+        check_lse(l, z["lse"], tag=f"plan W={wg}")
     o, l, _ = _gpu.run_uniform(db, int(z["num_chunks"]))
     check_out(o, z["out"], tag="uniform")
     check_lse(l, z["lse"], tag="uniform")

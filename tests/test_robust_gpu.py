@@ -56,7 +56,7 @@ def test_poisoned_tails_balanced(wg):
     bt = inputs.make_batch(POISON_LENS, 32, 8, seed=31)
     ro, rl = _ref(bt)
     _poison(bt)
-    o, l, info = _gpu.run_streamk(_gpu.DeviceBatch(bt), wg)
+    o, l, info = _gpu.run_plan(_gpu.DeviceBatch(bt), wg)
     check_out(o, ro, tag=f"poisoned balanced W={info.workgroups}")
     check_lse(l, rl, tag=f"poisoned balanced W={info.workgroups}")
 

@@ -41,14 +41,14 @@ def test_fake_shapes():
 @pytest.mark.gpu
 def test_paged_decode_op_matches_plan_and_oracle():
     from _checks import check_lse, check_out
-    from _gpu import DeviceBatch, run_streamk
+    from _gpu import DeviceBatch, run_plan
     bt = inputs.make_batch([3000, 1, 515, 0, 64], 32, 8, seed=41)
     q, k, v, ip, ix, la, iph, lah = _inputs_on("cuda:0", bt)
     print("op: paged_decode", flush=True)
     out, lse = torch.ops.pdattn.paged_decode(q, k, v, ip, ix, la, iph, lah, SCALE)
     torch.cuda.synchronize()
     db = DeviceBatch(bt)
-    o_ref, l_ref, _ = run_streamk(db)
+    o_ref, l_ref, _ = run_plan(db)
     assert np.array_equal(out.float().cpu().numpy(), o_ref)
     assert np.array_equal(lse.cpu().numpy().astype(np.float64), l_ref)
     ro, rl = oracle.decode(bt.q, bt.k, bt.v, bt.indptr, bt.indices, bt.last, 32, 8, threads=8)
