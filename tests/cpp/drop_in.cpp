@@ -23,6 +23,7 @@
 #include <cstdlib>
 #include <numeric>
 #include <random>
+#include <string>
 #include <vector>
 
 #include "pdattn.h"
@@ -221,6 +222,17 @@ void decode_case(const char* name, const std::vector<int>& lens, int Hq, int Hkv
     const int G = Hq / Hkv;
     const int max_len = *std::max_element(lens.begin(), lens.end());
     char tag[160];
+    // a caller that takes page tables from elsewhere checks them first: this one is valid, and
+    // the same table with one page id past the cache is refused
+    PD_OK(pdattn_check_page_table(b.indptr.data(), b.indices.data(), b.last.data(), b.B, b.pages));
+    if (b.pages > 0) {
+        std::vector<int32_t> bad = b.indices;
+        bad[bad.size() / 2] = b.pages;
+        const int st = pdattn_check_page_table(b.indptr.data(), bad.data(), b.last.data(), b.B, b.pages);
+        std::printf("%-52s %s\n", (std::string(name) + " page id past the cache refused").c_str(),
+                    st == PDATTN_ERR_PAGE_TABLE ? "PASS" : "FAIL");
+        if (st != PDATTN_ERR_PAGE_TABLE) ++g_failures;
+    }
     for (int force : {1, 0, 7}) {
         int nc = 0, ct = 0;
         PD_OK(pdattn_plan_chunks(G, 2, b.B, Hkv, max_len, force, &nc, &ct));
@@ -230,6 +242,12 @@ void decode_case(const char* name, const std::vector<int>& lens, int Hq, int Hkv
         std::snprintf(tag, sizeof tag, "%s decode_attention chunks=%d", name, nc);
         check(tag, b, db);
         pdattn_workspace_release(&ws);
+        // the same call for a caller that cannot allocate (partials in the library's own array)
+        if (pdattn_decode_workspace_size(b.B, Hq, nc) <= PDATTN_NOALLOC_SCRATCH_BYTES) {
+            PD_OK(pdattn_decode_attention_noalloc(&p, G, 2, db.out, db.lse, nullptr));
+            std::snprintf(tag, sizeof tag, "%s decode_attention_noalloc chunks=%d", name, nc);
+            check(tag, b, db);
+        }
     }
     pdattn_plan* plan = nullptr;
     PD_OK(pdattn_plan_create(b.indptr.data(), b.last.data(), b.B, Hq, Hkv, 0, 0, &plan));
