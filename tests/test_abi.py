@@ -183,3 +183,17 @@ def test_noalloc_rejects_partials_beyond_its_array():
     with pytest.raises(pdattn.PdattnError) as e:
         pdattn.decode_attention_noalloc(p, 4, 1 << 20, 1 << 20)
     assert e.value.status == 1
+
+
+@pytest.mark.parametrize("chunk_tokens", [0, 17, 8208])
+def test_cascade_prefix_rejects_chunk_sizes(chunk_tokens):
+    """Prefix chunks are whole pages, at most 8192 tokens (512 page ids staged per workgroup);
+    the check comes before any device work."""
+    pp = pdattn.PrefixParams()
+    pp.q = pp.k_cache = pp.v_cache = pp.prefix_pages = pp.part_o = pp.part_lse = 1 << 20
+    pp.B, pp.Hq, pp.Hkv = 2, 32, 8
+    pp.prefix_len, pp.chunk_tokens, pp.part_stride = 16384, chunk_tokens, 1024
+    pp.sm_scale = 0.088
+    with pytest.raises(pdattn.PdattnError) as e:
+        pdattn.cascade_prefix(pp)
+    assert e.value.status == 2   # PDATTN_ERR_UNSUPPORTED

@@ -59,13 +59,15 @@ def test_cascade_benchmark_config():
     check_lse(l2, rl, tag="non-shared plan")
 
 
-@pytest.mark.parametrize("chunk_tokens", [16, 64, 96, 1024])
-def test_prefix_kernel_partials(chunk_tokens):
-    """The MFMA prefix kernel alone: per-chunk partials over the shared keys."""
+@pytest.mark.parametrize("chunk_tokens,Lp", [(16, 640), (64, 640), (96, 640), (1024, 640), (8192, 8240)],
+                         ids=["16", "64", "96", "1024", "8192-max"])
+def test_prefix_kernel_partials(chunk_tokens, Lp):
+    """The MFMA prefix kernel alone: per-chunk partials over the shared keys (8192 tokens: the
+    largest chunk, 512 staged page ids, followed by a 48-token partial chunk)."""
     import torch
     import _gpu
     import pdattn
-    Lp = 640
+    print(f"[case] prefix kernel chunk_tokens={chunk_tokens} Lp={Lp}", flush=True)
     bt = inputs.make_shared_prefix_batch(Lp, [3, 20, 50], 32, 8, seed=8)
     db = _gpu.DeviceBatch(bt)
     nchunks = (Lp + chunk_tokens - 1) // chunk_tokens
