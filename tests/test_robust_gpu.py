@@ -4,7 +4,8 @@
   every last page, which a cache allocated with torch.empty and filled by appends leaves as they
   were, and with kv_start the slots before it): the result must not see them, on every decode
   path (balanced plan, uniform split, its long-chunk kernel, the cascade's suffix).
-* A negative or zero sm_scale: every path computes softmax(scale * q.k) as the oracle does.
+* A negative, zero or large sm_scale (scores in the hundreds, a softmax close to an argmax):
+  every path computes softmax(scale * q.k) as the oracle does.
 * Plans and workspaces: a plan whose uploaded schedule another upload or launch has written over
   is refused (PDATTN_ERR_NOT_READY) or, for the cascade (which uploads by itself), re-uploaded;
   never run on someone else's schedule.
@@ -134,7 +135,7 @@ def _cascade_with_scale(bt, db, scale, mode=None):
     return o, l, info
 
 
-@pytest.mark.parametrize("scale", [-SCALE, 0.0, -1.0])
+@pytest.mark.parametrize("scale", [-SCALE, 0.0, -1.0, 1.0, 8.0])
 def test_scale_sign_cascade_and_plan(scale):
     import torch
     import _gpu
