@@ -188,11 +188,13 @@ def size_matched_read_us(nbytes, stream, steps):
     return e0.elapsed_time(e1) * 1e3 / k
 
 
-def rotated_kernel_us(plan, ws, t, stream, steps):
-    """Average duration of one balanced launch, K launches back to back between one event pair.
+def rotated_kernel_us(plan, ws, t, stream, steps, parts=None):
+    """Average duration of one balanced step, K steps back to back between one event pair; with
+    `parts` (pdattn.RUN_DECODE or RUN_MERGE) only that launch of each step (pdattn_plan_run_part),
+    so that each kernel of the step is timed on its own. Returns (us, K, n).
 
-    Launch i reads K/V copy i mod n; the n copies total >= ROT_BYTES (4x the Infinity Cache), so
-    each launch reads lines no cache still holds, with no flush kernel between launches."""
+    Step i reads K/V copy i mod n; the n copies total >= ROT_BYTES (4x the Infinity Cache), so
+    each decode launch reads lines no cache still holds, with no flush kernel between launches."""
     import torch
     kv_bytes = 2 * t["k"].numel() * t["k"].element_size()
     n = max(2, -(-ROT_BYTES // kv_bytes))
@@ -202,8 +204,12 @@ def rotated_kernel_us(plan, ws, t, stream, steps):
         vs.append(torch.empty_like(t["v"]).normal_())
 
     def launch(i):
-        plan.run(t["q"], ks[i % n], vs[i % n], t["indptr"], t["indices"], t["last"], t["out"],
-                 t["lse"], ws, ws.numel(), stream=stream)
+        if parts is None:
+            plan.run(t["q"], ks[i % n], vs[i % n], t["indptr"], t["indices"], t["last"], t["out"],
+                     t["lse"], ws, ws.numel(), stream=stream)
+        else:
+            plan.run_part(parts, t["q"], ks[i % n], vs[i % n], t["indptr"], t["indices"], t["last"],
+                          t["out"], t["lse"], ws, ws.numel(), stream=stream)
     for i in range(n):
         launch(i)
     k = max(steps, 4 * n)
@@ -220,16 +226,20 @@ def rotated_kernel_us(plan, ws, t, stream, steps):
 
 
 def measured_traffic():
-    """HBM bytes per launch of the headline kernel from the committed counter summary
-    (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by its copy-kernel calibration), or None."""
+    """(HBM bytes per launch of the headline kernel, commit the counters were collected on) from the
+    committed counter summary (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by its copy-kernel
+    calibration), or (None, None)."""
+    nbytes, commit = None, None
     try:
         with open(TRAFFIC_FILE) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:"):
-                    return int(float(line.split(":", 1)[1]))
+                    nbytes = int(float(line.split(":", 1)[1]))
+                elif line.startswith("commit:"):
+                    commit = line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return None
+    return nbytes, commit
 
 
 def copy_calibration(steps):
@@ -299,8 +309,13 @@ def decode_workload(timer, lens, args, with_uniform, seed=11, nosplit=False):
     nbytes = bt.algorithmic_bytes()
     ms = statistics.median(times[0])
     kern_us, k, ncopy = rotated_kernel_us(plan, ws, t, s, args.steps)
+    import pdattn
+    dec_us, _, _ = rotated_kernel_us(plan, ws, t, s, args.steps, parts=pdattn.RUN_DECODE)
     info = plan.info()
+    mrg_us = (rotated_kernel_us(plan, ws, t, s, args.steps, parts=pdattn.RUN_MERGE)[0]
+              if info.merge_entries else 0.0)
     r = {"bytes": nbytes, "ms": ms, "steps": len(times[0]), "kernel_us": kern_us,
+         "decode_kernel_us": dec_us, "merge_kernel_us": mrg_us,
          "kernel_launches": k, "kv_copies": ncopy, "workgroups": info.workgroups,
          "split_pairs": info.split_pairs}
     if with_uniform:
@@ -329,6 +344,9 @@ def decode_leg(timer, lens, args, ceil, seed=11, reference=None):
            "kernel_us": round(h["kernel_us"], 2), "kernel_GB/s": round(a, 1),
            "kernel_pct_of_peak": round(100 * a / PEAK_GBS, 1),
            "kernel_pct_of_ceiling": round(100 * a / ceil, 1),
+           "decode_kernel_us": round(h["decode_kernel_us"], 2),
+           "merge_kernel_us": round(h["merge_kernel_us"], 2),
+           "decode_kernel_pct_of_peak": round(100 * gbs(h["bytes"], h["decode_kernel_us"] * 1e-6) / PEAK_GBS, 1),
            "uniform_path": h["uniform"], "no_split": h["no_split"]}
     for leg in (out["uniform_path"], out["no_split"]):
         leg["pct_of_peak"] = round(100 * leg["GB/s"] / PEAK_GBS, 1)
@@ -795,7 +813,8 @@ def main():
                         nosplit=args.only in ("", "32k", "64x1k"))
     value = gbs(h["bytes"], h["ms"] * 1e-3)
     achieved = gbs(h["bytes"], h["kernel_us"] * 1e-6)
-    traffic = measured_traffic() if not args.only or args.only == "32k" else None
+    traffic, traffic_commit = measured_traffic() if not args.only or args.only == "32k" else (None, None)
+    dec_achieved = gbs(h["bytes"], h["decode_kernel_us"] * 1e-6)
     result = dict(
         metric=METRIC, value=round(value, 1), unit="GB/s", n_gpus=1, steps=h["steps"],
         warmup=args.warmup, ms_per_step=round(h["ms"], 5), us_per_step=round(h["ms"] * 1e3, 2),
@@ -809,10 +828,17 @@ def main():
         roofline={"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                   "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
                   "traffic_source": (f"{os.path.relpath(TRAFFIC_FILE, ROOT)}: rocprofv3 --pmc FETCH_SIZE / "
-                                     "WRITE_SIZE of the decode launch, copy-calibrated" if traffic else None),
+                                     f"WRITE_SIZE of the decode launch, copy-calibrated, collected at "
+                                     f"commit {traffic_commit}" if traffic else None),
                   "kernel": "one decode step = decode_balanced_kernel + merge_split_kernel (the merge "
-                            "launch runs when pairs are split); frac is the whole step's, both launches",
+                            "launch runs when pairs are split); frac is the whole step's, both launches; "
+                            "kernel_frac is decode_balanced_kernel's alone (pdattn_plan_run_part, "
+                            "decode launches back to back in this run)",
                   "kernel_us": round(h["kernel_us"], 2),
+                  "kernel_frac": round(dec_achieved / PEAK_GBS, 4),
+                  "decode_kernel_us": round(h["decode_kernel_us"], 2),
+                  "decode_kernel_GB/s": round(dec_achieved, 1),
+                  "merge_kernel_us": round(h["merge_kernel_us"], 2),
                   "timing": f"{h['kernel_launches']} back-to-back steps over {h['kv_copies']} "
                             f"K/V copies (>= 1 GiB) between one event pair"},
         device={"arch": dinfo.arch.decode(), "cus": dinfo.compute_units},
@@ -826,6 +852,7 @@ def main():
         result["stream_read_ceiling_GBs"] = round(ceil, 1)
         result["pct_of_ceiling"] = round(100 * value / ceil, 1)
         result["roofline"]["frac_of_ceiling"] = round(achieved / ceil, 4)
+        result["roofline"]["kernel_frac_of_ceiling"] = round(dec_achieved / ceil, 4)
         sm_us = size_matched_read_us(h["bytes"], timer.stream, args.steps)
         result["roofline"]["size_matched_read"] = {
             "bytes": h["bytes"], "us": round(sm_us, 2), "GB/s": round(gbs(h["bytes"], sm_us * 1e-6), 1),

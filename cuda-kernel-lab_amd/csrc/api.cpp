@@ -182,6 +182,15 @@ std::atomic<uint64_t> g_next_owner{1};
 
 uint64_t new_owner() { return g_next_owner.fetch_add(1); }
 
+// A plan's schedule tag: a mix of its owner id with the high bit set, so that it is never a small
+// integer, a float's usual bit pattern or a fill value such as 0 or -1.
+int32_t schedule_tag(uint64_t id) {
+    uint64_t x = (id + 0x9E3779B97F4A7C15ull) * 0xBF58476D1CE4E5B9ull;
+    x ^= x >> 31;
+    const uint32_t t = (uint32_t)(x >> 32) | 0x80000000u;
+    return (int32_t)(t == 0xFFFFFFFFu ? 0x8A5A5A5Au : t);
+}
+
 void res_drop_locked(uintptr_t lo, uintptr_t hi, uint64_t keep) {
     g_res.erase(std::remove_if(g_res.begin(), g_res.end(),
                                [&](const Resident& r) { return r.owner != keep && r.lo < hi && lo < r.hi; }),
@@ -244,12 +253,17 @@ struct pdattn_plan {
     int ngroups = 0;                  // > 0: page-range partition of that many groups
     int64_t U = 0;
     int split_pairs = 0, max_contrib = 0, n_entries = 0, n_slots = 0, segments = 0;
+    int cmax = 0;                     // > 0: partial slots laid out by merge entry (e * cmax + k)
     // workspace layout (bytes from the base)
     size_t off_desc = 0, off_list = 0, off_plse = 0, off_po = 0, ws_bytes = 0;
     std::vector<int32_t> host_blob;   // desc[W * kBalDescInts] followed by the merge list
     void* pinned = nullptr;           // pinned copy of host_blob for stream-ordered upload
     size_t blob_bytes = 0;
     uint64_t id = new_owner();        // owner of its uploaded schedules (resident-schedule records)
+    // Written into every descriptor block and the merge list header, and passed to the kernels,
+    // which leave a block or list that does not carry it alone (bytes written over since the
+    // upload by something the resident-schedule records cannot see).
+    int32_t tag = schedule_tag(id);
 };
 
 // One node of a shared-prefix tree: the ns sequences seqs[seq_off ..] all hold the same physical
@@ -449,9 +463,14 @@ int build_balanced_plan(const int32_t* indptr, const int32_t* last, int B, int H
         W = std::min<int64_t>(U, W * 2);
     }
 
-    // partial slots and merge list: pairs in (b, kv head) order, contributors in unit order
+    // partial slots and merge list: pairs in (b, kv head) order, contributors in unit order.
+    // Packed, contributor k of a listed pair is slot slot0 + k with the pairs' slots consecutive;
+    // laid out by entry (cmax = the most contributors of a listed pair), contributor k of entry e
+    // is slot e * cmax + k, which the merge can address before it has read the entry. The entry
+    // layout is used unless it would take more than twice the packed slots (a few long pairs among
+    // many short ones).
     std::vector<int32_t> slot0(pairs, -1), list;
-    int slots = 0, split = 0, mx = 1;
+    int slots = 0, split = 0, mx = 1, cmax = 0;
     auto need_slots = [&](size_t pr) { return nc[pr] > 1 || (merge_all && nc[pr] > 0); };
     for (int b = 0; b < B; ++b)
         for (int kvh = 0; kvh < Hkv; ++kvh) {
@@ -461,11 +480,23 @@ int build_balanced_plan(const int32_t* indptr, const int32_t* last, int B, int H
             if (need_slots(pr)) {
                 slot0[pr] = slots;
                 slots += nc[pr];
+                cmax = std::max(cmax, nc[pr]);
                 list.insert(list.end(), {b, kvh, slot0[pr], nc[pr]});
             } else if (nc[pr] == 0) {
                 list.insert(list.end(), {b, kvh, 0, 0});   // empty sequence: extras only, or 0 / -inf
             }
         }
+    const int64_t n_list = (int64_t)(list.size() / 4);
+    if (cmax > 0 && n_list * cmax <= 2 * (int64_t)slots + 64) {
+        for (int64_t e = 0; e < n_list; ++e) {
+            const size_t pr = (size_t)list[4 * e] * Hkv + list[4 * e + 1];
+            list[4 * e + 2] = (int32_t)(e * cmax);
+            if (slot0[pr] >= 0) slot0[pr] = (int32_t)(e * cmax);
+        }
+        slots = (int)(n_list * cmax);
+    } else {
+        cmax = 0;
+    }
     std::vector<int> seen(pairs, 0);
     for (const SegRef& rf : refs) {
         int32_t* sg = &desc[(size_t)rf.w * kBalDescInts + 8 + kSegInts * rf.idx];
@@ -478,13 +509,16 @@ int build_balanced_plan(const int32_t* indptr, const int32_t* last, int B, int H
     pl->max_contrib = mx;
     pl->n_entries = (int)(list.size() / 4);
     pl->n_slots = slots;
+    pl->cmax = cmax;
     pl->segments = (int)refs.size();
+    for (int64_t w = 0; w < W; ++w) desc[(size_t)w * kBalDescInts + 1] = pl->tag;
     pl->host_blob = desc;
+    pl->host_blob.insert(pl->host_blob.end(), {pl->tag, pl->n_entries, cmax, 0});   // list header
     pl->host_blob.insert(pl->host_blob.end(), list.begin(), list.end());
 
     size_t off = 0;
     pl->off_desc = off;  off += align_up(sizeof(int32_t) * desc.size());
-    pl->off_list = off;  off += align_up(sizeof(int32_t) * std::max<size_t>(4, list.size()));
+    pl->off_list = off;  off += align_up(sizeof(int32_t) * (4 + list.size()));
     pl->off_plse = off;  off += align_up(sizeof(float) * std::max(1, slots) * G);
     pl->off_po = off;    off += align_up(sizeof(float) * std::max(1, slots) * G * kHeadDim);
     pl->ws_bytes = off;
@@ -518,9 +552,8 @@ int upload_plan(pdattn_plan* pl, void* ws, size_t bytes, hipStream_t s) {
     }
     if (pl->blob_bytes) {
         PD_HIP(hipMemcpyAsync(base + pl->off_desc, pl->pinned, desc_bytes, hipMemcpyHostToDevice, s));
-        if (pl->n_entries)
-            PD_HIP(hipMemcpyAsync(base + pl->off_list, static_cast<char*>(pl->pinned) + desc_bytes,
-                                  sizeof(int32_t) * 4 * pl->n_entries, hipMemcpyHostToDevice, s));
+        PD_HIP(hipMemcpyAsync(base + pl->off_list, static_cast<char*>(pl->pinned) + desc_bytes,
+                              sizeof(int32_t) * 4 * (1 + pl->n_entries), hipMemcpyHostToDevice, s));
     }
     res_claim(base + pl->off_desc, schedule_bytes(pl), pl->id);
     return PDATTN_OK;
@@ -547,17 +580,19 @@ BalArgs bal_args(const pdattn_plan* pl, const void* q, const void* k, const void
     a.part_stride = 0;   // the planner's slot-major partials
     a.ngroups = pl->ngroups;
     a.nnz = pl->nnz;
+    a.tag = pl->tag;
     return a;
 }
 
 // Balanced decode launch, then (when the plan lists any) the merge launch. With `join`, the
 // stream waits for that event between the two (the extra partials come from another stream).
 // decode = false: the decode workgroups ran elsewhere (the fused cascade step); merge only.
+// merge = false: the decode launch only (pdattn_plan_run_part).
 int run_plan(const pdattn_plan* pl, const void* q, const void* k, const void* v,
              const int32_t* indptr, const int32_t* indices, const int32_t* last, float sm_scale,
              void* out, float* lse, void* ws, size_t bytes, hipStream_t s,
              const float* extra_o = nullptr, const float* extra_lse = nullptr, int n_extra = 0,
-             hipEvent_t join = nullptr, bool decode = true) {
+             hipEvent_t join = nullptr, bool decode = true, bool merge = true) {
     if (!ws || !res_holds(static_cast<char*>(ws) + pl->off_desc, schedule_bytes(pl), pl->id))
         return fail(PDATTN_ERR_NOT_READY,
                     "plan's schedule is not in this workspace (never uploaded there, or overwritten "
@@ -578,7 +613,7 @@ int run_plan(const pdattn_plan* pl, const void* q, const void* k, const void* v,
     if (pl->U > 0 && decode)
         PD_HIP(launch_decode_balanced(bal_args(pl, q, k, v, indices, sm_scale, out, lse, base), pl->G, s));
     if (join) PD_HIP(hipStreamWaitEvent(s, join, 0));
-    if (pl->n_entries) {
+    if (pl->n_entries && merge) {
         MergeArgs m;
         m.list = reinterpret_cast<const int32_t*>(base + pl->off_list);
         m.part_o = part_o;
@@ -587,9 +622,14 @@ int run_plan(const pdattn_plan* pl, const void* q, const void* k, const void* v,
         m.extra_lse = extra_lse;
         m.out = static_cast<_Float16*>(out);
         m.lse = lse;
+        m.B = pl->B;
         m.Hq = pl->Hq;
+        m.Hkv = pl->Hkv;
         m.G = pl->G;
         m.n_extra = n_extra;
+        m.cmax = pl->cmax;
+        m.n_slots = pl->n_slots;
+        m.tag = pl->tag;
         PD_HIP(launch_merge_split(m, pl->n_entries, s));
     }
     return PDATTN_OK;
@@ -935,6 +975,7 @@ static int launch_uniform_split(const PartialArgs& a, int G, hipStream_t s) {
     d.part_stride = a.part_stride;
     d.ngroups = 0;
     d.nnz = 0;
+    d.tag = 0;   // (descriptors built in the kernel: no tag to check)
     u.kv_indptr = a.kv_indptr;
     u.kv_last = a.kv_last;
     u.kv_start = a.kv_start;
@@ -1093,6 +1134,18 @@ int pdattn_plan_run(const pdattn_plan* pl, const void* q, const void* k_cache, c
     if (!pl) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null plan");
     return run_plan(pl, q, k_cache, v_cache, kv_indptr, kv_indices, kv_last_page_len, sm_scale,
                     out, lse, workspace, bytes, static_cast<hipStream_t>(stream));
+}
+
+int pdattn_plan_run_part(const pdattn_plan* pl, const void* q, const void* k_cache, const void* v_cache,
+                         const int32_t* kv_indptr, const int32_t* kv_indices,
+                         const int32_t* kv_last_page_len, float sm_scale, void* out, float* lse,
+                         void* workspace, size_t bytes, void* stream, int parts) {
+    if (!pl) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null plan");
+    if (parts < PDATTN_RUN_DECODE || parts > PDATTN_RUN_ALL)
+        return fail(PDATTN_ERR_INVALID_ARGUMENT, "parts=%d not in 1..3", parts);
+    return run_plan(pl, q, k_cache, v_cache, kv_indptr, kv_indices, kv_last_page_len, sm_scale,
+                    out, lse, workspace, bytes, static_cast<hipStream_t>(stream), nullptr, nullptr, 0,
+                    nullptr, (parts & PDATTN_RUN_DECODE) != 0, (parts & PDATTN_RUN_MERGE) != 0);
 }
 
 void pdattn_plan_destroy(pdattn_plan* pl) {

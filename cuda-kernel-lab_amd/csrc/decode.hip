@@ -424,59 +424,129 @@ __device__ __forceinline__ void lse_accumulate(float& m, float& ws, float4& acc,
     acc.w = fmaf(w, o.w, acc.w);
 }
 
-// Log-sum-exp merge of one row from `nsrc` partial states in a fixed order (merge_states,
-// 01_decode_attention.cu:238-255): each of TPQ threads per 4-dim quad takes every TPQ-th source,
-// issuing four independent 16-byte loads at a time and accumulating them online; the TPQ states
-// of a quad are then combined in thread order through LDS. The result does not depend on the order
-// in which the sources were produced. load(k, l, o) fetches source k's lse and its quad of o. A row
-// whose every source is empty gets out = 0, lse = -inf.
+// Log-sum-exp merge of one row (128 dims) from partial states in a fixed order (merge_states,
+// 01_decode_attention.cu:238-255), by one workgroup of kMergeThreads = 4 waves, with no LDS and no
+// barrier. The sources are two lists, A then B (a pair's partial slots, then a cascade row's prefix
+// partials): source k of a list has its lse at lse[k * stride] and its output row at
+// o[k * stride * 128]. Wave w covers dims [32 w, 32 w + 32): lane 8 q + r holds the 4 dims
+// 32 w + 4 q .. of sources r, r + 8, r + 16, ... of each list. The first 32 sources of both lists
+// are loaded before any is waited for (one round trip), each lane folds its sources in order (A's,
+// then B's), and the 8 source lanes of a quad are then combined by three DPP exchanges (lane
+// distances 1, 2, then the other quad of the 8-lane half row): a fixed order, so the result is
+// deterministic. keepA(k), evaluated after the loads, drops source k of A (a slot the decode launch
+// did not write). The state is left in every lane: merged output acc / ws, lse m + ln ws.
 constexpr int kMergeThreads = 256;
-template <class Load>
-__device__ __forceinline__ void merge_row(int nsrc, Load load, float* red, _Float16* out_row, float* lse_out) {
-    constexpr int Q = kHeadDim / 4, TPQ = kMergeThreads / Q;
-    const int tid = threadIdx.x, quad = tid % Q, r = tid / Q;
-    float m = -INFINITY, ws = 0.f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int k = r; k < nsrc; k += 4 * TPQ) {
-        float l[4];
-        float4 o[4];
+constexpr int kMergeU = 4;   // sources of a list per lane per round trip
+struct MState {
+    float m, ws;
+    float4 acc;
+};
+struct MSrc {
+    const float* lse;
+    const float* o;
+    size_t stride;
+    int n;
+};
+
+template <int CTRL>
+__device__ __forceinline__ void mstate_fold_dpp(MState& s) {
+    const float m2 = dpp<CTRL>(s.m), w2 = dpp<CTRL>(s.ws);
+    const float x2 = dpp<CTRL>(s.acc.x), y2 = dpp<CTRL>(s.acc.y);
+    const float z2 = dpp<CTRL>(s.acc.z), u2 = dpp<CTRL>(s.acc.w);
+    const float M = fmaxf(s.m, m2);
+    const float s1 = (s.m == -INFINITY) ? 0.f : fast_exp2((s.m - M) * kLog2e);
+    const float s2 = (m2 == -INFINITY) ? 0.f : fast_exp2((m2 - M) * kLog2e);
+    s.ws = s.ws * s1 + w2 * s2;
+    s.acc.x = s.acc.x * s1 + x2 * s2;
+    s.acc.y = s.acc.y * s1 + y2 * s2;
+    s.acc.z = s.acc.z * s1 + z2 * s2;
+    s.acc.w = s.acc.w * s1 + u2 * s2;
+    s.m = M;
+}
+
+__device__ __forceinline__ int merge_d0() { return 32 * (int)(threadIdx.x >> 6) + 4 * (int)((threadIdx.x & 63) >> 3); }
+
+// Loads sources k0 + r + 8 u (u < kMergeU) of list S (S.n > 0), unconditionally: a lane past the
+// last source reloads the last one, so every lane issues the same loads and no load waits for
+// another (conditional loads would make the compiler copy the results, and wait for them, where
+// the branches join).
+__device__ __forceinline__ void merge_load(const MSrc& S, int k0, float (&l)[kMergeU], float4 (&o)[kMergeU]) {
+    const int r = threadIdx.x & 7, d0 = merge_d0();
 #pragma unroll
-        for (int u = 0; u < 4; ++u) load(min(k + u * TPQ, nsrc - 1), 4 * quad, l[u], o[u]);
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
-            if (k + u * TPQ < nsrc) lse_accumulate(m, ws, acc, l[u], o[u]);
+    for (int u = 0; u < kMergeU; ++u) {
+        const size_t i = (size_t)min(k0 + r + 8 * u, S.n - 1) * S.stride;
+        l[u] = S.lse[i];
+        o[u] = *reinterpret_cast<const float4*>(S.o + i * kHeadDim + d0);
     }
-    float* rd = red + tid * 6;
-    rd[0] = m;
-    rd[1] = ws;
-    rd[2] = acc.x;
-    rd[3] = acc.y;
-    rd[4] = acc.z;
-    rd[5] = acc.w;
-    __syncthreads();
-    if (r == 0) {
-        for (int rr = 1; rr < TPQ; ++rr) {
-            const float* o = red + (rr * Q + quad) * 6;
-            if (o[1] > 0.f) {
-                // fold in a partial state (o[0] + ln o[1], o[2..5] / o[1])
-                const float mm = fmaxf(m, o[0]);
-                const float sa = fast_exp2((m - mm) * kLog2e), sb = fast_exp2((o[0] - mm) * kLog2e);
-                ws = ws * sa + o[1] * sb;
-                acc.x = acc.x * sa + o[2] * sb;
-                acc.y = acc.y * sa + o[3] * sb;
-                acc.z = acc.z * sa + o[4] * sb;
-                acc.w = acc.w * sa + o[5] * sb;
-                m = mm;
-            }
+}
+// Folds this lane's loaded sources into s in order, branch-free (a dropped or empty source weighs 0
+// and its values are replaced, not multiplied, so unused slots may hold anything): with every
+// loaded value used unconditionally, the compiler keeps all the loads ahead of the first wait.
+// For a kept source this is the online rule of lse_accumulate: the running state is rescaled by
+// exp(m - max(m, l)) (exactly 1 when l <= m) and the source added with weight exp(l - max(m, l)).
+template <class Keep>
+__device__ __forceinline__ void merge_fold(MState& s, const MSrc& S, int k0, const float (&l)[kMergeU],
+                                           const float4 (&o)[kMergeU], Keep keep) {
+    const int r = threadIdx.x & 7;
+#pragma unroll
+    for (int u = 0; u < kMergeU; ++u) {
+        const int k = k0 + r + 8 * u;
+        const bool ok = k < S.n && keep(k) && l[u] != -INFINITY;
+        const float lv = ok ? l[u] : -INFINITY;
+        const float4 ov = ok ? o[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float mn = fmaxf(s.m, lv);
+        const float sc = (s.m == -INFINITY) ? 0.f : fast_exp2((s.m - mn) * kLog2e);
+        const float w = ok ? fast_exp2((lv - mn) * kLog2e) : 0.f;
+        s.ws = fmaf(s.ws, sc, w);
+        s.acc.x = fmaf(w, ov.x, s.acc.x * sc);
+        s.acc.y = fmaf(w, ov.y, s.acc.y * sc);
+        s.acc.z = fmaf(w, ov.z, s.acc.z * sc);
+        s.acc.w = fmaf(w, ov.w, s.acc.w * sc);
+        s.m = mn;
+    }
+}
+
+template <class KeepA>
+__device__ __forceinline__ MState merge_lanes(const MSrc& A, const MSrc& B, KeepA keepA) {
+    constexpr int SPT = 8 * kMergeU;   // sources of a list per round trip
+    MState s{-INFINITY, 0.f, make_float4(0.f, 0.f, 0.f, 0.f)};
+    float la[kMergeU], lb[kMergeU];
+    float4 oa[kMergeU], ob[kMergeU];
+    auto all = [](int) { return true; };
+    if (A.n > 0) merge_load(A, 0, la, oa);
+    if (B.n > 0) merge_load(B, 0, lb, ob);
+    __builtin_amdgcn_sched_barrier(0);   // every load above is issued before anything waits
+    if (A.n > 0) {
+        merge_fold(s, A, 0, la, oa, keepA);
+        for (int k0 = SPT; k0 < A.n; k0 += SPT) {
+            merge_load(A, k0, la, oa);
+            merge_fold(s, A, k0, la, oa, keepA);
         }
-        const float inv = ws > 0.f ? 1.f / ws : 0.f;
-        _Float16* op = out_row + 4 * quad;
-        op[0] = (_Float16)(acc.x * inv);
-        op[1] = (_Float16)(acc.y * inv);
-        op[2] = (_Float16)(acc.z * inv);
-        op[3] = (_Float16)(acc.w * inv);
-        if (quad == 0) *lse_out = ws > 0.f ? m + fast_log2(ws) * kLn2 : -INFINITY;
     }
+    if (B.n > 0) {
+        merge_fold(s, B, 0, lb, ob, all);
+        for (int k0 = SPT; k0 < B.n; k0 += SPT) {
+            merge_load(B, k0, lb, ob);
+            merge_fold(s, B, k0, lb, ob, all);
+        }
+    }
+    mstate_fold_dpp<0xB1>(s);    // quad_perm [1,0,3,2]
+    mstate_fold_dpp<0x4E>(s);    // quad_perm [2,3,0,1]
+    mstate_fold_dpp<0x141>(s);   // row_half_mirror: the other quad of the 8-lane half row
+    return s;
+}
+
+// Writes a merged row: lane 0 of each 8-lane group its 4 fp16 outputs, the first of them the lse.
+// A row whose every source is empty gets out = 0, lse = -inf.
+__device__ __forceinline__ void merge_store(const MState& s, _Float16* out_row, float* lse_out) {
+    if ((threadIdx.x & 7) != 0) return;
+    const int d0 = merge_d0();
+    const float inv = s.ws > 0.f ? 1.f / s.ws : 0.f;
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 hv = {(_Float16)(s.acc.x * inv), (_Float16)(s.acc.y * inv), (_Float16)(s.acc.z * inv),
+                   (_Float16)(s.acc.w * inv)};
+    *reinterpret_cast<h4*>(out_row + d0) = hv;
+    if (d0 == 0) *lse_out = s.ws > 0.f ? s.m + fast_log2(s.ws) * kLn2 : -INFINITY;
 }
 
 // ---- uniform chunks: the reference's decode_partial launch shape -------------------------
@@ -518,40 +588,52 @@ __global__ __launch_bounds__(kMergeThreads) void merge_states_kernel(const float
                                                                       _Float16* __restrict__ out,
                                                                       float* __restrict__ lse_out,
                                                                       int num_chunks) {
-    __shared__ float red[kMergeThreads * 6];
     const size_t row = blockIdx.x;
-    const float* pl = part_lse + row * num_chunks;
-    const float* po = part_o + row * num_chunks * kHeadDim;
-    merge_row(num_chunks,
-              [&](int k, int d0, float& l, float4& o) {
-                  l = pl[k];
-                  o = *reinterpret_cast<const float4*>(po + (size_t)k * kHeadDim + d0);
-              },
-              red, out + row * kHeadDim, lse_out + row);
+    const MSrc A{part_lse + row * num_chunks, part_o + row * num_chunks * kHeadDim, 1, num_chunks};
+    const MSrc B{part_lse, part_o, 1, 0};
+    const MState st = merge_lanes(A, B, [](int) { return true; });
+    merge_store(st, out + row * kHeadDim, lse_out + row);
 }
 
 // ---- balanced launch -------------------------------------------------------------------------
 // Merge of the pairs listed by the planner: one workgroup per row (entry, head). Sources: the
-// pair's partial slots in order, then the row's extra partials (cascade prefix chunks).
+// pair's partial slots in order, then the row's extra partials (cascade prefix chunks). A list
+// whose header does not carry the launch's tag, or an entry outside the batch or the workspace's
+// slots, is someone else's bytes: the row is left alone.
+// RECT (slots laid out by entry, cmax > 0): the list header, the entry and every partial are loaded
+// in one round trip (the header and entry as vector loads through a zero lane offset the compiler
+// cannot see through, so that they count against the same counter as the partials and nothing is
+// waited for before all are issued). Otherwise the partials follow the entry.
+template <bool RECT>
 __global__ __launch_bounds__(kMergeThreads) void merge_split_kernel(MergeArgs a) {
-    __shared__ float red[kMergeThreads * 6];
-    const int e = blockIdx.x / a.G, h = blockIdx.x % a.G;
-    const int b = a.list[4 * e], kvh = a.list[4 * e + 1], slot0 = a.list[4 * e + 2], nc = a.list[4 * e + 3];
-    const int G = a.G, n_extra = a.n_extra;
-    const size_t row = (size_t)b * a.Hq + (size_t)kvh * G + h;
-    merge_row(nc + n_extra,
-              [&](int k, int d0, float& l, float4& o) {
-                  if (k < nc) {
-                      const size_t sl = (size_t)(slot0 + k) * G + h;
-                      l = a.part_lse[sl];
-                      o = *reinterpret_cast<const float4*>(a.part_o + sl * kHeadDim + d0);
-                  } else {
-                      const size_t ex = row * n_extra + (k - nc);
-                      l = a.extra_lse[ex];
-                      o = *reinterpret_cast<const float4*>(a.extra_o + ex * kHeadDim + d0);
-                  }
-              },
-              red, a.out + row * kHeadDim, a.lse + row);
+    const int G = a.G, e = blockIdx.x / G, h = blockIdx.x - e * G;
+    int z = 0;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+    // header {tag, n_entries, cmax, 0} and entry {b, kvh, slot0, nc}
+    const int4 hd = *reinterpret_cast<const int4*>(a.list + z);
+    const int4 en = *reinterpret_cast<const int4*>(a.list + 4 + 4 * (size_t)e + z);
+    const int n_extra = a.n_extra;
+    MState st;
+    if constexpr (RECT) {
+        const int cmax = a.cmax;
+        const size_t sl0 = (size_t)e * cmax * G + h;   // slot e * cmax, head h
+        const size_t row = (size_t)e * G + h;          // with extra partials entry e is pair e
+        const MSrc A{a.part_lse + sl0, a.part_o + sl0 * kHeadDim, (size_t)G, cmax};
+        const MSrc B{a.extra_lse + row * n_extra, a.extra_o + row * n_extra * kHeadDim, 1, n_extra};
+        st = merge_lanes(A, B, [&](int k) { return k < en.w; });
+        if (en.w > cmax || (n_extra > 0 && (int64_t)en.x * a.Hkv + en.y != (int64_t)e)) return;
+    } else {
+        if (hd.x != a.tag || en.z < 0 || en.w < 0 || (int64_t)en.z + en.w > a.n_slots) return;
+        if (en.x < 0 || en.x >= a.B || en.y < 0 || en.y >= a.Hkv) return;
+        const size_t sl0 = (size_t)en.z * G + h;
+        const size_t row = ((size_t)en.x * a.Hkv + en.y) * G + h;
+        const MSrc A{a.part_lse + sl0, a.part_o + sl0 * kHeadDim, (size_t)G, en.w};
+        const MSrc B{a.extra_lse + row * n_extra, a.extra_o + row * n_extra * kHeadDim, 1, n_extra};
+        st = merge_lanes(A, B, [](int) { return true; });
+    }
+    if (hd.x != a.tag || en.x < 0 || en.x >= a.B || en.y < 0 || en.y >= a.Hkv) return;
+    const size_t orow = ((size_t)en.x * a.Hkv + en.y) * G + h;
+    merge_store(st, a.out + orow * kHeadDim, a.lse + orow);
 }
 
 // Per-segment merge scratch of the balanced kernel: the raw online-softmax state of every row
@@ -775,7 +857,11 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
         __syncthreads();
         PD_STAMP(1);
         nseg = __builtin_amdgcn_readfirstlane(sd[0]);
-        if (nseg <= 0) return;   // uniform: every thread leaves
+        // (uniform: every thread leaves) no segment, or not this plan's descriptor block: the
+        // workspace was written over since the upload, and nothing here is to be trusted
+        if (nseg <= 0 || nseg > BalShared<C, COMPACT>::SEGS ||
+            __builtin_amdgcn_readfirstlane(sd[1]) != kargs()->tag)
+            return;
     } else {
         // items w, w + W, ...: thread t builds the descriptor of the t-th (the decode_partial
         // rule, 01_decode_attention.cu:88-97: keys [kv_start + chunk * chunk_tokens, + chunk_tokens)
@@ -883,8 +969,12 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
         }
         int pv[PMAX];
         if constexpr (!RANGES) {
+            // (unconditional within the list, so one round trip; none at all for a workgroup whose
+            // items hold no page, whose kv_indices may be empty)
+            if (npages > 0) {
 #pragma unroll
-            for (int k = 0; k < PMAX; ++k) pv[k] = kvi[max(src[k], 0)];   // (unconditional: one round trip)
+                for (int k = 0; k < PMAX; ++k) pv[k] = kvi[max(src[k], 0)];
+            }
         } else {
             seek();
 #pragma unroll
@@ -1086,7 +1176,8 @@ int occupancy_cascade_step(int G) { PD_DISPATCH_RET(BalCfg, G, occ_step); }
 
 hipError_t launch_merge_split(const MergeArgs& a, int n_entries, hipStream_t s) {
     if (n_entries <= 0) return hipSuccess;
-    merge_split_kernel<<<n_entries * a.G, kMergeThreads, 0, s>>>(a);
+    if (a.cmax > 0) merge_split_kernel<true><<<n_entries * a.G, kMergeThreads, 0, s>>>(a);
+    else merge_split_kernel<false><<<n_entries * a.G, kMergeThreads, 0, s>>>(a);
     return hipGetLastError();
 }
 

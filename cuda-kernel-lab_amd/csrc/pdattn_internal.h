@@ -35,7 +35,8 @@ struct PartialArgs {
 // default range g of the page sequence cut into W / Hkv equal ranges for workgroup g * Hkv + h,
 // kv head h; or the units [U w / W, U (w+1) / W) of the pairs' chunks, kv head fastest -- cut into
 // segments (one per sequence or chunk piece), described in desc[w * kBalDescInts ..]:
-//   desc[0] = number of segments; segment s at desc[8 + kSegInts * s] =
+//   desc[0] = number of segments; desc[1] = the plan's tag (a launch whose tag argument differs
+//   finds someone else's bytes there and does nothing); segment s at desc[8 + kSegInts * s] =
 //   {b, kvh, qa, npg, t0, t1, jpos, slot}: sequence b, kv head kvh, pages [qa, qa + npg) of the
 //   workgroup's page list, tokens [t0, t1) of the sequence (t0 = first token of its first page),
 //   page-table position jpos of its first page (relative to kv_indptr[0]), and the partial slot
@@ -66,6 +67,7 @@ struct BalArgs {
     // [nnz g / ngroups, nnz (g + 1) / ngroups) of kv_indices (its page list, in order)
     int ngroups;
     int nnz;
+    int tag;                      // the plan's tag, expected in desc[1] of every block (host plans)
 };
 
 // The reference-shaped uniform split (decode_partial / decode_attention) run by the balanced
@@ -81,18 +83,25 @@ struct UniArgs {
     int kv_start, chunk_tokens, num_chunks, chunk_base, n_items, per_wg;
 };
 
-// Merge of split pairs (and of every pair when extra partials are given): entry e of `list` is
-// {b, kvh, slot0, nc}: the nc >= 0 partial slots slot0 .. slot0 + nc - 1 of the pair, in order,
-// then the n_extra extra partials of each of its G rows.
+// Merge of split pairs (and of every pair when extra partials are given). `list` starts with a
+// header {tag, n_entries, cmax, 0}; entry e (at list[4 + 4 e]) is {b, kvh, slot0, nc}: the
+// nc >= 0 partial slots slot0 .. slot0 + nc - 1 of the pair, in order, then the n_extra extra
+// partials of each of its G rows. With cmax > 0 the slots are laid out by entry, slot0 = e * cmax
+// (nc <= cmax), so the partials' addresses do not depend on the list and are loaded in the same
+// round trip as the entry. With n_extra > 0 the list holds every pair in (b, kvh) order: entry e is
+// pair e, so its rows (and their extra partials) are known from e as well.
 struct MergeArgs {
-    const int32_t*  list;         // [n_entries * 4]
+    const int32_t*  list;         // [4 + n_entries * 4]
     const float*    part_o;
     const float*    part_lse;
     const float*    extra_o;      // [B*Hq, n_extra, 128] or null
     const float*    extra_lse;    // [B*Hq, n_extra]
     _Float16*       out;
     float*          lse;
-    int Hq, G, n_extra;
+    int B, Hq, Hkv, G, n_extra;
+    int cmax;                     // > 0: slots laid out by entry (see above)
+    int n_slots;                  // partial slots in the workspace (a listed range beyond is refused)
+    int tag;                      // expected in the list header (else the launch does nothing)
 };
 
 // Paged KV append: token t (of n) of sequence batch_idx[t] at position positions[t].

@@ -40,7 +40,8 @@ EXPORTS = [
     "pdattn_decode_workspace_size", "pdattn_workspace_partials", "pdattn_decode_attention",
     "pdattn_decode_attention_noalloc",
     "pdattn_plan_create", "pdattn_plan_get_info", "pdattn_plan_workspace_size",
-    "pdattn_plan_get_schedule", "pdattn_plan_upload", "pdattn_plan_run", "pdattn_plan_destroy",
+    "pdattn_plan_get_schedule", "pdattn_plan_upload", "pdattn_plan_run", "pdattn_plan_run_part",
+    "pdattn_plan_destroy",
     "pdattn_shared_prefix_pages", "pdattn_cascade_prefix",
     "pdattn_cascade_plan_create", "pdattn_cascade_tree_plan_create", "pdattn_cascade_plan_get_info",
     "pdattn_cascade_decode", "pdattn_cascade_set_mode",
@@ -104,6 +105,7 @@ class CascadeInfo(ctypes.Structure):
 
 # pdattn_cascade_set_mode
 CASCADE_FUSED, CASCADE_SERIAL, CASCADE_TWO_STREAMS = 0, 1, 2
+RUN_DECODE, RUN_MERGE, RUN_ALL = 1, 2, 3   # pdattn_plan_run_part
 
 
 class DeviceInfo(ctypes.Structure):
@@ -151,6 +153,7 @@ def lib():
         "pdattn_plan_workspace_size": ([P], S),
         "pdattn_plan_upload": ([P, P, S, P], I),
         "pdattn_plan_run": ([P, P, P, P, P, P, P, ctypes.c_float, P, P, P, S, P], I),
+        "pdattn_plan_run_part": ([P, P, P, P, P, P, P, ctypes.c_float, P, P, P, S, P, I], I),
         "pdattn_plan_destroy": ([P], None),
         "pdattn_shared_prefix_pages": ([P, P, I], I),
         "pdattn_cascade_prefix": ([ctypes.POINTER(PrefixParams), P], I),
@@ -306,9 +309,11 @@ class Plan:
         _check(lib().pdattn_plan_get_info(self._h, ctypes.byref(inf)), "pdattn_plan_get_info")
         return inf
 
-    def schedule(self):
+    def schedule(self, with_header: bool = False):
         """(segments, merge_list): segments[w] is a list of 8-int segments
-        {b, kvh, qa, npg, t0, t1, jpos, slot}; merge_list is an (n, 4) array {b, kvh, slot0, nc}."""
+        {b, kvh, qa, npg, t0, t1, jpos, slot}; merge_list is an (n, 4) array {b, kvh, slot0, nc}.
+        with_header: also the merge list's header {tag, n_entries, cmax, 0} (cmax > 0: contributor
+        k of entry e is slot e * cmax + k)."""
         import numpy as np
         inf = self.info()
         buf = np.zeros(inf.schedule_ints, dtype=np.int32)
@@ -319,7 +324,10 @@ class Plan:
         for w in range(W):
             d = buf[w * SCHEDULE_WG_INTS:(w + 1) * SCHEDULE_WG_INTS]
             segs.append([d[8 + 8 * i:16 + 8 * i].tolist() for i in range(int(d[0]))])
-        return segs, buf[W * SCHEDULE_WG_INTS:].reshape(-1, 4)
+        lst = buf[W * SCHEDULE_WG_INTS:].reshape(-1, 4)
+        if with_header:
+            return segs, lst[1:], lst[0].tolist()
+        return segs, lst[1:]
 
     @property
     def workspace_bytes(self) -> int:
@@ -336,6 +344,15 @@ class Plan:
                                      ptr(kv_indices), ptr(kv_last_page_len), ctypes.c_float(sc),
                                      ptr(out), ptr(lse), ptr(workspace), nbytes, stream_ptr(stream)),
                "pdattn_plan_run")
+
+    def run_part(self, parts: int, q, k_cache, v_cache, kv_indptr, kv_indices, kv_last_page_len, out,
+                 lse, workspace, nbytes: int, sm_scale=None, stream=None):
+        """pdattn_plan_run_part: RUN_DECODE, RUN_MERGE or RUN_ALL (for timing each launch)."""
+        sc = (1.0 / HEAD_DIM ** 0.5) if sm_scale is None else sm_scale
+        _check(lib().pdattn_plan_run_part(self._h, ptr(q), ptr(k_cache), ptr(v_cache), ptr(kv_indptr),
+                                          ptr(kv_indices), ptr(kv_last_page_len), ctypes.c_float(sc),
+                                          ptr(out), ptr(lse), ptr(workspace), nbytes, stream_ptr(stream),
+                                          parts), "pdattn_plan_run_part")
 
     def close(self):
         if self._h:

@@ -19,7 +19,9 @@
  *   kv_indptr [B+1], kv_indices [nnz], kv_last_page_len [B]   int32 CSR page table (FlashInfer)
  *   out        [B, Hq, 128] fp16;  lse [B, Hq] fp32 (natural log of the scaled scores)
  * q head h reads kv head h / G with G = Hq / Hkv in {1, 2, 4, 8}; head_dim is 128; page size 16.
- * An empty sequence (no pages) yields out = 0, lse = -inf.
+ * An empty sequence (no pages) yields out = 0, lse = -inf. kv_indices is read only at the
+ * positions [kv_indptr[b], kv_indptr[b+1]) of the sequences' pages: when every sequence is empty
+ * it may point at a buffer of no elements (but not be NULL).
  */
 #ifndef PDATTN_H
 #define PDATTN_H
@@ -187,10 +189,14 @@ int pdattn_plan_create(const int32_t* h_kv_indptr, const int32_t* h_kv_last_page
                        int Hq, int Hkv, int force_workgroups, int chunk_pages, pdattn_plan** plan);
 int pdattn_plan_get_info(const pdattn_plan* plan, pdattn_plan_info* info);
 size_t pdattn_plan_workspace_size(const pdattn_plan* plan);
-/* Copy of the plan's schedule (info.schedule_ints int32): per workgroup, the segment count then
- * up to 24 segments of 8 ints {b, kvh, offset in the workgroup's page list, pages, first token,
- * end token, page-table position of the first page (relative to kv_indptr[0]), partial slot or
- * -1}, 200 ints per workgroup; then the merge list, 4 ints per entry {b, kvh, first slot, slots}.
+/* Copy of the plan's schedule (info.schedule_ints int32): per workgroup, the segment count, the
+ * plan's tag, 6 unused ints, then up to 24 segments of 8 ints {b, kvh, offset in the workgroup's
+ * page list, pages, first token, end token, page-table position of the first page (relative to
+ * kv_indptr[0]), partial slot or -1}, 200 ints per workgroup; then the merge list: a header
+ * {tag, entries, cmax, 0} and 4 ints per entry {b, kvh, first slot, slots}. With cmax > 0 the
+ * partial slots are laid out by entry (entry e's first slot is e * cmax), so that the merge
+ * launch loads the entry and the partials in one round trip. The kernels leave a descriptor
+ * block or merge list alone whose tag is not the plan's.
  * For inspection and tests; `count` must be at least info.schedule_ints. */
 int pdattn_plan_get_schedule(const pdattn_plan* plan, int32_t* out, size_t count);
 /* Stream-ordered copy of the plan's schedule into `workspace`. Must precede pdattn_plan_run with
@@ -199,7 +205,10 @@ int pdattn_plan_get_schedule(const pdattn_plan* plan, int32_t* out, size_t count
  * same memory): pdattn_plan_run then returns PDATTN_ERR_NOT_READY instead of running on what it
  * finds there, and the plan is uploaded again. Writes the library does not make (the caller's own
  * kernels or copies into the workspace, or its memory freed and allocated again at the same
- * address) are not seen: after those the caller uploads again. */
+ * address) are not seen by those records: after them the caller uploads again. A run over such
+ * bytes computes nothing and writes nothing, since every descriptor block and the merge list
+ * carry the plan's tag, which the kernels check (a run therefore needs its upload, not only a
+ * workspace of the right size). */
 int pdattn_plan_upload(pdattn_plan* plan, void* workspace, size_t bytes, void* stream);
 /* Attention for every (sequence, q head) of the planned batch: the decode launch and, when the
  * plan has split pairs or empty sequences, the merge launch. The device page table must hold the
@@ -209,6 +218,17 @@ int pdattn_plan_run(const pdattn_plan* plan, const void* q, const void* k_cache,
                     const void* v_cache, const int32_t* kv_indptr, const int32_t* kv_indices,
                     const int32_t* kv_last_page_len, float sm_scale, void* out, float* lse,
                     void* workspace, size_t bytes, void* stream);
+/* Measurement hook (no counterpart in the reference, whose harness times whole calls): the same
+ * run, making only some of its launches -- PDATTN_RUN_DECODE the decode launch (split pairs leave
+ * their partials in the workspace, out / lse of split pairs are not written), PDATTN_RUN_MERGE
+ * the merge launch over the partials already in the workspace, PDATTN_RUN_ALL both, which is
+ * pdattn_plan_run. For timing each kernel of a step on its own (bench.py); a result is complete
+ * only after both parts have run, in that order. */
+enum { PDATTN_RUN_DECODE = 1, PDATTN_RUN_MERGE = 2, PDATTN_RUN_ALL = 3 };
+int pdattn_plan_run_part(const pdattn_plan* plan, const void* q, const void* k_cache,
+                         const void* v_cache, const int32_t* kv_indptr, const int32_t* kv_indices,
+                         const int32_t* kv_last_page_len, float sm_scale, void* out, float* lse,
+                         void* workspace, size_t bytes, void* stream, int parts);
 void pdattn_plan_destroy(pdattn_plan* plan);
 
 /* ---- shared-prefix (cascade) path --------------------------------------------------------- */

@@ -8,7 +8,10 @@ checked against a brute-force restatement of the partition contract in pdattn.h:
     its range, in order;
   * a pair with more than one segment gets consecutive partial slots, its k-th segment (in unit
     order) writing slot slot0 + k, and one merge-list entry; a pair with one segment writes the
-    final output (slot -1); an empty sequence gets a merge entry with no slots.
+    final output (slot -1); an empty sequence gets a merge entry with no slots;
+  * the slots are then laid out by merge entry (entry e's k-th slot is e * cmax + k, cmax = the
+    most slots of an entry) unless that takes more than twice the packed slots plus 64, and the
+    merge list's header says which {tag, entries, cmax or 0, 0}.
 """
 import numpy as np
 import pytest
@@ -67,6 +70,32 @@ def brute_schedule(indptr, last, Hkv, W, P):
     return U, segs, merge, split, mx
 
 
+def entry_layout(segs, merge):
+    """The slots of a packed schedule moved to the layout by merge entry, where that costs at most
+    twice the packed slots plus 64: entry e's k-th slot becomes e * cmax + k. Returns cmax (0: the
+    packed layout is kept)."""
+    packed = sum(m[3] for m in merge)
+    cmax = max([m[3] for m in merge] + [0])
+    if cmax == 0 or len(merge) * cmax > 2 * packed + 64:
+        return 0
+    remap = {}
+    for e, m in enumerate(merge):
+        for k in range(m[3]):
+            remap[m[2] + k] = e * cmax + k
+        m[2] = e * cmax
+    for ss in segs:
+        for sg in ss:
+            if sg[7] >= 0:
+                sg[7] = remap[sg[7]]
+    return cmax
+
+
+def check_header(plan, merge, cmax):
+    _, _, hd = plan.schedule(with_header=True)
+    assert hd[0] != 0 and hd[0] < 0          # the plan's tag (high bit set)
+    assert hd[1:] == [len(merge), cmax, 0]
+
+
 CASES = [
     ([32768], 8),
     ([1024] * 64, 8),
@@ -90,16 +119,18 @@ def test_schedule_matches_contract(lens, Hkv, W, P):
     Wp = info.workgroups
     assert Wp >= min(W, info.units)              # grows only to respect per-workgroup limits
     U, segs, merge, split, mx = brute_schedule(bt.indptr, bt.last, Hkv, Wp, P)
+    slots = sum(m[3] for m in merge)
+    cmax = entry_layout(segs, merge)
     got_segs, got_merge = plan.schedule()
     assert info.units == U
     assert got_segs == segs
     assert got_merge.tolist() == merge
+    check_header(plan, merge, cmax)
     assert info.split_pairs == split and info.max_contributors == mx
     assert info.pairs == bt.B * Hkv
     assert info.segments == sum(len(s) for s in segs)
     assert info.merge_entries == len(merge)
-    slots = sum(m[3] for m in merge)
-    assert info.workspace_bytes >= slots * 4 * 129 * 4
+    assert info.workspace_bytes >= max(slots, len(merge) * cmax) * 4 * 129 * 4
     # every (page, kv head) unit exactly once
     seen = set()
     for ss in got_segs:
@@ -165,9 +196,11 @@ def test_grouped_schedule_matches_contract(lens, Hkv, W):
     Wp = info.workgroups
     assert Wp % Hkv == 0
     segs, merge = brute_grouped(bt.indptr, bt.last, Hkv, Wp)
+    cmax = entry_layout(segs, merge)
     got_segs, got_merge = plan.schedule()
     assert got_segs == segs
     assert got_merge.tolist() == merge
+    check_header(plan, merge, cmax)
     for g in range(Wp // Hkv):
         ranges = [[(s[0], s[2], s[3], s[6]) for s in got_segs[g * Hkv + h]] for h in range(Hkv)]
         assert all(r == ranges[0] for r in ranges)

@@ -8,7 +8,12 @@
   every path computes softmax(scale * q.k) as the oracle does.
 * Plans and workspaces: a plan whose uploaded schedule another upload or launch has written over
   is refused (PDATTN_ERR_NOT_READY) or, for the cascade (which uploads by itself), re-uploaded;
-  never run on someone else's schedule.
+  never run on someone else's schedule. A workspace the caller writes over itself (random bytes,
+  or another plan's schedule copied in from torch), which the library cannot see, fails the tag
+  check of the decode and merge kernels: the run writes nothing, and the plan is correct again
+  after its next upload.
+* An all-empty batch whose kv_indices points at the end of a buffer (no element): nothing reads
+  it, and every row is 0 / -inf.
 """
 import numpy as np
 import pytest
@@ -316,3 +321,93 @@ def test_cascade_plans_share_one_workspace():
         for p in plans.values():
             p.close()
         pdattn.workspace_release(ws)
+
+
+@pytest.mark.parametrize("what", ["random bytes", "another plan's schedule"])
+def test_plan_workspace_written_by_the_caller(what):
+    """The caller overwrites an uploaded plan's workspace with torch (unseen by the library's
+    records): the run's kernels find a descriptor block and merge list without the plan's tag and
+    leave out / lse as they were; after a new upload the plan is correct again."""
+    import torch
+    import pdattn
+    print(f"[case] plan workspace overwritten from torch with {what}", flush=True)
+    btA, dbA, A, (roA, rlA) = _plan_batch([300, 5000, 17], 48, 64)
+    btB, dbB, B, _ = _plan_batch([2048] * 3, 49, 64)
+    n = max(A.workspace_bytes, B.workspace_bytes) + 4096
+    ws = torch.zeros(n, dtype=torch.uint8, device="cuda:0")
+    A.upload(ws, n)
+    o, l = _run(A, dbA, ws)
+    check_out(o, roA, tag="A before")
+    assert A.info().merge_entries > 0          # both kernels of the run are exercised
+    if what == "random bytes":
+        g = torch.Generator(device="cuda:0")
+        g.manual_seed(50)
+        ws.copy_(torch.randint(0, 256, (n,), dtype=torch.uint8, device="cuda:0", generator=g))
+    else:
+        ws2 = torch.zeros_like(ws)
+        B.upload(ws2, n)
+        torch.cuda.synchronize()
+        ws.copy_(ws2)                            # B's schedule, where A's was
+    dbA.out.fill_(7.0)
+    dbA.lse.fill_(7.0)
+    _run(A, dbA, ws)                             # the library's records still hold A's upload
+    torch.cuda.synchronize()
+    assert bool((dbA.out == 7.0).all()) and bool((dbA.lse == 7.0).all()), \
+        "a run over someone else's bytes wrote results"
+    A.upload(ws, n)
+    o, l = _run(A, dbA, ws)
+    check_out(o, roA, tag="A after its re-upload")
+    check_lse(l, rlA, tag="A after its re-upload")
+    A.close()
+    B.close()
+
+
+def test_all_empty_batch_with_an_empty_page_list():
+    """Every sequence empty and kv_indices pointing just past the end of a buffer (no element):
+    the uniform split (one chunk and several), the plan path and decode_partial run without
+    reading it, and every row is 0 / -inf."""
+    import torch
+    import pdattn
+    print("[case] all-empty batch, kv_indices at the end of its buffer", flush=True)
+    d = torch.device("cuda:0")
+    B, Hq, Hkv = 5, 32, 8
+    q = torch.randn(B, Hq, 128, device=d).half()
+    k = torch.zeros(1, 16, Hkv, 128, dtype=torch.float16, device=d)
+    v = torch.zeros_like(k)
+    indptr = torch.zeros(B + 1, dtype=torch.int32, device=d)
+    last = torch.zeros(B, dtype=torch.int32, device=d)
+    holder = torch.zeros(64, dtype=torch.int32, device=d)
+    indices = holder.data_ptr() + holder.numel() * 4   # no element: the address just past `holder`
+    out = torch.empty(B, Hq, 128, dtype=torch.float16, device=d)
+    lse = torch.empty(B, Hq, dtype=torch.float32, device=d)
+
+    def check(tag):
+        torch.cuda.synchronize()
+        assert bool((out == 0).all()), tag
+        assert bool(torch.isinf(lse).all()) and bool((lse < 0).all()), tag
+
+    for nc in (1, 3):
+        out.fill_(7.0)
+        lse.fill_(7.0)
+        p = pdattn.make_params(q, k, v, indptr, indices, last, B, Hq, Hkv, nc, 16)
+        ws = pdattn.Workspace()
+        try:
+            pdattn.decode_attention(p, 4, out, lse, ws)
+            check(f"decode_attention, {nc} chunks")
+        finally:
+            pdattn.workspace_release(ws)
+    plan = pdattn.Plan([0] * (B + 1), [0] * B, B, Hq, Hkv)
+    wsp = torch.zeros(max(256, plan.workspace_bytes), dtype=torch.uint8, device=d)
+    plan.upload(wsp, wsp.numel())
+    out.fill_(7.0)
+    lse.fill_(7.0)
+    plan.run(q, k, v, indptr, indices, last, out, lse, wsp, wsp.numel())
+    check("plan path")
+    plan.close()
+    po = torch.full((B * Hq, 2, 128), float("nan"), dtype=torch.float32, device=d)
+    pl = torch.full((B * Hq, 2), float("nan"), dtype=torch.float32, device=d)
+    p = pdattn.make_params(q, k, v, indptr, indices, last, B, Hq, Hkv, 2, 16, 0, 0, 2, None, po, pl)
+    pdattn.decode_partial(p, 4)
+    torch.cuda.synchronize()
+    assert bool(torch.isinf(pl).all()) and bool((pl < 0).all())
+    assert bool((po == 0).all())

@@ -1,6 +1,8 @@
 """The timeline build of the library (make -C cuda-kernel-lab_amd timeline: the kernels compiled
 with per-workgroup timestamps, read by bench.py --timeline) computes exactly what the library
-proper computes, and its stamps come in phase order.
+proper computes, and its stamps come in phase order: the plan path's decode, the fused cascade
+step (decode and prefix roles, then the merge) and the prefix kernel alone with a partial last
+chunk, each compared bit for bit.
 
 The timeline build is loaded in a child process, so this process keeps the library proper.
 """
@@ -36,7 +38,8 @@ CHILD = textwrap.dedent(r"""
 
     print("[case] timeline build vs library, lens=[3000, 17, 700]", flush=True)
     bt = inputs.make_batch([3000, 17, 700], 32, 8, seed=51)
-    _, o0, l0, _ = run(os.path.join(sys.argv[1], "cuda-kernel-lab_amd", "lib", "libpdattn.so"), bt)
+    lib0 = os.path.join(sys.argv[1], "cuda-kernel-lab_amd", "lib", "libpdattn.so")
+    _, o0, l0, _ = run(lib0, bt)
     L, o1, l1, info = run(sys.argv[2], bt)
     assert np.array_equal(o0, o1) and np.array_equal(l0, l1), "timeline build changed the results"
     L.pdattn_timeline_read_decode.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
@@ -49,6 +52,59 @@ CHILD = textwrap.dedent(r"""
         seq = [row[0], row[1], row[2]] + [row[s] for s in range(4, 28) if row[s] > 0] + [row[31]]
         assert all(b >= a for a, b in zip(seq, seq[1:])), f"stamps out of order: {seq}"
     print("ok", int(ran.sum()), "workgroups stamped", flush=True)
+
+    # the fused cascade step (decode role and prefix role in one launch, both stamped) and the
+    # merge after it
+    print("[case] fused cascade step, timeline build vs library, prefix 1024 + 40 x 77", flush=True)
+    bc = inputs.make_shared_prefix_batch(1024, [77] * 40, 32, 8, seed=13)
+    res = []
+    for path in (lib0, sys.argv[2]):
+        pdattn._lib = None
+        pdattn.LIB_PATH = path
+        pdattn.lib()
+        o, l, ci = _gpu.run_cascade(_gpu.DeviceBatch(bc), min_prefix=16)
+        assert ci.use == 1 and ci.mode == pdattn.CASCADE_FUSED, (ci.use, ci.mode)
+        res.append((o, l))
+    assert np.array_equal(res[0][0], res[1][0]) and np.array_equal(res[0][1], res[1][1]), \
+        "timeline build changed the fused cascade step's results"
+
+    # the prefix kernel alone, with a partial last chunk (640 keys in chunks of 96: 6 full + 64)
+    print("[case] prefix kernel, timeline build vs library, 640 keys in chunks of 96", flush=True)
+    bp = inputs.make_shared_prefix_batch(640, [3, 20, 50], 32, 8, seed=8)
+    nch, rows = 7, bp.B * bp.Hq
+    res = []
+    for path in (lib0, sys.argv[2]):
+        pdattn._lib = None
+        pdattn.LIB_PATH = path
+        Lp = pdattn.lib()
+        if path != lib0:
+            assert Lp.pdattn_timeline_reset_prefix() == 0
+        db = _gpu.DeviceBatch(bp)
+        po = torch.full((rows, nch, 128), float("nan"), dtype=torch.float32, device="cuda:0")
+        pl = torch.full((rows, nch), float("nan"), dtype=torch.float32, device="cuda:0")
+        pp = pdattn.PrefixParams()
+        pp.q, pp.k_cache, pp.v_cache = db.q.data_ptr(), db.k.data_ptr(), db.v.data_ptr()
+        pp.prefix_pages = db.indices.data_ptr()
+        pp.part_o, pp.part_lse = po.data_ptr(), pl.data_ptr()
+        pp.B, pp.Hq, pp.Hkv = bp.B, bp.Hq, bp.Hkv
+        pp.prefix_len, pp.chunk_tokens, pp.part_stride = 640, 96, nch
+        pp.sm_scale = 1.0 / np.sqrt(128)
+        pdattn.cascade_prefix(pp)
+        torch.cuda.synchronize()
+        res.append((po.cpu().numpy(), pl.cpu().numpy()))
+    assert np.array_equal(res[0][0].view(np.int32), res[1][0].view(np.int32)) and \
+        np.array_equal(res[0][1].view(np.int32), res[1][1].view(np.int32)), \
+        "timeline build changed the prefix kernel's partials"
+    Lp.pdattn_timeline_read_prefix.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    buf = np.zeros(8192 * 32, np.uint64)
+    assert Lp.pdattn_timeline_read_prefix(buf.ctypes.data, buf.nbytes) == 0
+    nwg = nch * 1 * bp.Hkv          # grid (chunks, query groups = 1, kv heads)
+    t = buf.reshape(8192, 32)[:nwg].astype(np.int64)
+    assert (t[:, 0] > 0).all(), "a prefix workgroup left no stamps"
+    for row in t:
+        seq = [row[0], row[1], row[2]] + [row[s] for s in range(3, 27) if row[s] > 0] + [row[29], row[30]]
+        assert all(b >= a for a, b in zip(seq, seq[1:])), f"prefix stamps out of order: {seq}"
+    print("ok prefix", nwg, "workgroups stamped", flush=True)
 """)
 
 
@@ -57,4 +113,4 @@ def test_timeline_build_matches_library_and_stamps_in_order():
     r = subprocess.run([sys.executable, "-c", CHILD, ROOT, TL_LIB], capture_output=True, text=True,
                        timeout=110)
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
-    assert "ok" in r.stdout
+    assert "ok prefix" in r.stdout
