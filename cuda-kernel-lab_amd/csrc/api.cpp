@@ -1081,6 +1081,115 @@ int pdattn_decode_attention(const pdattn_decode_params* p, int G, int variant, v
     return decode_attention_launch(p, G, out, lse, part_o, part_lse, static_cast<hipStream_t>(stream));
 }
 
+}  // extern "C"
+
+namespace {
+
+// Layout of the device-range decode (pdattn_decode_attention_balanced): the grid, ranges and the
+// workspace, or use_uniform when the batch is past the kernel's staging (kDevMaxB sequences).
+struct DevLayout {
+    bool use_uniform = false;
+    int W = 0, NG = 0;
+    int64_t span = 0;
+    size_t off_prefix = 0, off_plse = 0, off_po = 0, bytes = 0;
+};
+
+int dev_layout(const pdattn_decode_params* p, int G, DevLayout* L) {
+    *L = DevLayout();
+    if (p->B > kDevMaxB) {
+        L->use_uniform = true;
+        L->bytes = pdattn_decode_workspace_size(p->B, p->Hq, p->part_stride);
+        return PDATTN_OK;
+    }
+    DeviceFacts f;
+    if (int st = device_facts(&f)) return st;
+    // one workgroup per CU (two at G = 8, as the plan path), whole groups of Hkv; more ranges if a
+    // range could hold more pages than the kernel stages (kRangeMax): every sequence attends at
+    // most ceil(span / 16) + 1 pages
+    L->span = (int64_t)p->num_chunks * p->chunk_tokens;
+    const int64_t per_seq = L->span / kPage + 2;
+    const int64_t bound = (int64_t)p->B * per_seq;
+    int64_t NG = std::max<int64_t>(1, (int64_t)f.cus * (G > 4 ? 2 : 1) / p->Hkv);
+    NG = std::max<int64_t>(NG, (bound + kRangeMax - 1) / kRangeMax);
+    if (NG * p->Hkv > (1 << 24)) return fail(PDATTN_ERR_INVALID_ARGUMENT, "too many ranges");
+    L->NG = (int)NG;
+    L->W = (int)(NG * p->Hkv);
+    const size_t slots = (size_t)2 * L->W * G;
+    size_t off = 0;
+    L->off_prefix = off; off += align_up(sizeof(int32_t) * (p->B + 1));
+    L->off_plse = off;   off += align_up(sizeof(float) * slots);
+    L->off_po = off;     off += align_up(sizeof(float) * slots * kHeadDim);
+    L->bytes = off;
+    return PDATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t pdattn_decode_balanced_workspace_size(const pdattn_decode_params* p, int G) {
+    if (!p || check_decode_params(p, G) != PDATTN_OK) return 0;
+    if (p->B == 0) return 0;
+    DevLayout L;
+    if (dev_layout(p, G, &L) != PDATTN_OK) return 0;
+    return L.bytes;
+}
+
+int pdattn_decode_attention_balanced(const pdattn_decode_params* p, int G, int variant, void* out,
+                                     float* lse, pdattn_workspace* ws, void* stream) {
+    if (variant < 0 || variant > 3) return fail(PDATTN_ERR_INVALID_ARGUMENT, "variant %d not in 0..3", variant);
+    if (int st = check_decode_params(p, G)) return st;
+    if (p->B == 0) return PDATTN_OK;
+    if (!out || !lse) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null out / lse");
+    DevLayout L;
+    if (int st = dev_layout(p, G, &L)) return st;
+    if (L.use_uniform) return pdattn_decode_attention(p, G, variant, out, lse, ws, stream);
+    if (int st = ensure_ws(ws, L.bytes)) return st;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    char* base = static_cast<char*>(ws->base);
+    res_written(base, L.bytes);
+    res_written_outputs(out, lse, (size_t)p->B * p->Hq);
+    DevArgs a;
+    BalArgs& d = a.d;
+    d.q = static_cast<const _Float16*>(p->q);
+    d.k = static_cast<const uint8_t*>(p->k_cache);
+    d.v = static_cast<const uint8_t*>(p->v_cache);
+    d.kv_indices = p->kv_indices;
+    d.out = static_cast<_Float16*>(out);
+    d.lse = lse;
+    d.desc = nullptr;
+    d.part_o = reinterpret_cast<float*>(base + L.off_po);
+    d.part_lse = reinterpret_cast<float*>(base + L.off_plse);
+    d.B = p->B;
+    d.Hq = p->Hq;
+    d.Hkv = p->Hkv;
+    d.W = L.W;
+    d.scale_log2 = p->sm_scale * 1.4426950408889634f;
+    d.part_stride = 0;
+    d.ngroups = L.NG;
+    d.nnz = 0;
+    d.tag = 0;   // (descriptors built in the kernel: no tag to check)
+    a.kv_indptr = p->kv_indptr;
+    a.kv_last = p->kv_last_page_len;
+    a.prefix = reinterpret_cast<int32_t*>(base + L.off_prefix);
+    a.span = L.span;
+    a.kv_start = p->kv_start;
+    PD_HIP(launch_decode_ranges(a, G, s));
+    DevMergeArgs m;
+    m.prefix = a.prefix;
+    m.part_o = d.part_o;
+    m.part_lse = d.part_lse;
+    m.out = d.out;
+    m.lse = lse;
+    m.B = p->B;
+    m.Hq = p->Hq;
+    m.Hkv = p->Hkv;
+    m.G = G;
+    m.ngroups = L.NG;
+    PD_HIP(launch_merge_ranges(m, s));
+    return PDATTN_OK;
+}
+
 int pdattn_plan_create(const int32_t* h_kv_indptr, const int32_t* h_kv_last_page_len, int B,
                        int Hq, int Hkv, int force_workgroups, int chunk_pages, pdattn_plan** plan) {
     if (!plan) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null plan output");

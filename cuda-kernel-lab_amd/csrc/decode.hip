@@ -798,107 +798,25 @@ struct BalShared {
     int sd[kBalDescInts];                          // descriptor block: header, then segments
 };
 
-// The body of one balanced-decode workgroup w (the kernel's argument block must start with the
-// BalArgs `a`, which kargs() reads).
-template <class C, bool UNI = false, bool COMPACT = false, bool RANGES = false>
-__device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COMPACT>& S, int w,
-                                              const UniArgs* u = nullptr) {
-    static_assert(!(UNI && RANGES), "the uniform split builds its own descriptors");
+// The segments staged in S.sd (nseg of them, at most S's SEGS; page ids of a page-range plan
+// already in S.pg): their q rows and, for other plans, their page ids (positions from the
+// descriptors, in kv_indices of the argument block) are loaded in one round trip, then every
+// wave streams its pages of all segments through one ring, flushing each segment at its end.
+// All threads of the workgroup call it.
+template <class C, bool COMPACT, bool RANGES>
+__device__ __forceinline__ void run_segments(const BalArgs& a, BalShared<C, COMPACT>& S, int nseg) {
     constexpr int G = C::G, NW = C::NW, NT = C::NT, NBUF = C::NBUF, LPR = C::LPR;
     auto& sm = S.sm;
     int* pg = S.pg;
     auto& qs = S.qs;
     int* sd = S.sd;
-    // the wave index is made wave-uniform explicitly: everything the page ring derives from it
-    // (per-wave page counts, page ids, buffer resources) must live in scalar registers
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane / LPR, c = lane % LPR;
-    // Segment fields are staged in LDS and read back wave-uniform: global (vector) loads of them
-    // would count against the same wait counter as the ring's page loads, and a non-uniform value
-    // in a buffer resource would turn every page load into a loop over lanes. sd holds the
-    // descriptor block: a header of 8 ints, then the segments.
     int* seg = sd + 8;
     auto fld = [&](int si, int f) { return __builtin_amdgcn_readfirstlane(seg[si * kSegInts + f]); };
-    // timestamps (timeline build only): 0 start, 1 descriptors (and page ids) staged, 2 q rows
-    // staged, 3 the first ring step computed, 4 + 2 s / 5 + 2 s segment s streamed / flushed
-    // (s < 12), 31 done; thread 0 of the workgroup
-    PD_STAMP(0);
     constexpr int PMAX = kRangeMax / NT, QPS = G * kHeadDim / 8;
     constexpr int QMAX = (BalShared<C, COMPACT>::SEGS * QPS + NT - 1) / NT;
-    // A page-range plan (RANGES: ngroups > 0) gives workgroup w = g * Hkv + kvh the pages
-    // [lo, hi) of the page table (relative to kv_indptr[0]), lo = nnz g / ngroups: its page list is
-    // known from the kernel arguments, so the page ids are loaded together with the descriptor
-    // block, and the ring's first pages together with the q rows.
-    int64_t lo = 0, hi = 0;
-    if constexpr (RANGES) {
-        const int64_t g = w / a.Hkv, nnz = kargs()->nnz, ng = kargs()->ngroups;
-        lo = nnz * g / ng;
-        hi = nnz * (g + 1) / ng;
-    }
-    int nseg;
-    if constexpr (!UNI) {
-        // round trip 1: the whole descriptor block (one int per thread), and the page ids of a
-        // page-range plan
-        const int32_t* desc = kargs()->desc + (size_t)w * kBalDescInts;
-        const int32_t* kvi = kargs()->kv_indices + lo;   // (pointers read from the arguments once)
-        const int dv = tid < kBalDescInts ? desc[tid] : 0;
-        int pv[PMAX];
-        const int npr = (int)(hi - lo);
-#pragma unroll
-        for (int k = 0; k < PMAX; ++k) {
-            const int i = tid + k * NT;
-            pv[k] = i < npr ? kvi[i] : 0;
-        }
-        if (tid < kBalDescInts) sd[tid] = dv;
-#pragma unroll
-        for (int k = 0; k < PMAX; ++k)
-            if (tid + k * NT < npr) pg[tid + k * NT] = pv[k];
-        __syncthreads();
-        PD_STAMP(1);
-        nseg = __builtin_amdgcn_readfirstlane(sd[0]);
-        // (uniform: every thread leaves) no segment, or not this plan's descriptor block: the
-        // workspace was written over since the upload, and nothing here is to be trusted
-        if (nseg <= 0 || nseg > BalShared<C, COMPACT>::SEGS ||
-            __builtin_amdgcn_readfirstlane(sd[1]) != kargs()->tag)
-            return;
-    } else {
-        // items w, w + W, ...: thread t builds the descriptor of the t-th (the decode_partial
-        // rule, 01_decode_attention.cu:88-97: keys [kv_start + chunk * chunk_tokens, + chunk_tokens)
-        // clipped to the sequence; an empty range writes 0 / -inf). t0 is the first key of the
-        // range, which need not start a page: keys are numbered from its page's first token.
-        nseg = min(u->per_wg, (u->n_items - w + a.W - 1) / a.W);
-        if (nseg <= 0) return;   // uniform: the host sizes the grid so that every workgroup has items
-        if (tid < nseg) {
-            const int item = w + tid * a.W;
-            const int pair = item / u->num_chunks, chunk = item - pair * u->num_chunks;
-            const int b = pair / a.Hkv, kvh = pair - b * a.Hkv;
-            const int pb = u->kv_indptr[b], np = u->kv_indptr[b + 1] - pb;
-            // (a last-page length outside [1, 16] is clamped: no key past the sequence's pages)
-            const int len = np > 0 ? (np - 1) * kPage + min(kPage, max(1, u->kv_last[b])) : 0;
-            const int kbeg = u->kv_start + chunk * u->chunk_tokens;
-            const int kend = max(kbeg, min(len, kbeg + u->chunk_tokens));
-            const int pf = kbeg / kPage;
-            int* sg = seg + tid * kSegInts;
-            sg[0] = b;
-            sg[1] = kvh;
-            sg[3] = kend > kbeg ? (kend - 1) / kPage - pf + 1 : 0;
-            sg[4] = kbeg;
-            sg[5] = kend;
-            sg[6] = pb + pf;
-            sg[7] = a.out != nullptr ? -1 : u->chunk_base + chunk;
-        }
-        __syncthreads();
-        // page-list offsets: exclusive prefix sum of the page counts
-        if (tid < nseg) {
-            int qa = 0;
-            for (int j = 0; j < tid; ++j) qa += seg[j * kSegInts + 3];
-            seg[tid * kSegInts + 2] = qa;
-        }
-        __syncthreads();
-        PD_STAMP(1);
-    }
-
     const uint32_t page_bytes = (uint32_t)(kPage * a.Hkv * 256);
     const uint32_t lbase = (uint32_t)(r * a.Hkv * 256 + c * 16);
     const uint32_t rstride = (uint32_t)(C::RPI * a.Hkv * 256);
@@ -1035,6 +953,286 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
     PD_STAMP(31);
 }
 
+
+// The body of one balanced-decode workgroup w (the kernel's argument block must start with the
+// BalArgs `a`, which kargs() reads).
+template <class C, bool UNI = false, bool COMPACT = false, bool RANGES = false>
+__device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COMPACT>& S, int w,
+                                              const UniArgs* u = nullptr) {
+    static_assert(!(UNI && RANGES), "the uniform split builds its own descriptors");
+    constexpr int G = C::G, NW = C::NW, NT = C::NT, NBUF = C::NBUF, LPR = C::LPR;
+    auto& sm = S.sm;
+    int* pg = S.pg;
+    auto& qs = S.qs;
+    int* sd = S.sd;
+    // the wave index is made wave-uniform explicitly: everything the page ring derives from it
+    // (per-wave page counts, page ids, buffer resources) must live in scalar registers
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane / LPR, c = lane % LPR;
+    // Segment fields are staged in LDS and read back wave-uniform: global (vector) loads of them
+    // would count against the same wait counter as the ring's page loads, and a non-uniform value
+    // in a buffer resource would turn every page load into a loop over lanes. sd holds the
+    // descriptor block: a header of 8 ints, then the segments.
+    int* seg = sd + 8;
+    auto fld = [&](int si, int f) { return __builtin_amdgcn_readfirstlane(seg[si * kSegInts + f]); };
+    // timestamps (timeline build only): 0 start, 1 descriptors (and page ids) staged, 2 q rows
+    // staged, 3 the first ring step computed, 4 + 2 s / 5 + 2 s segment s streamed / flushed
+    // (s < 12), 31 done; thread 0 of the workgroup
+    PD_STAMP(0);
+    constexpr int PMAX = kRangeMax / NT, QPS = G * kHeadDim / 8;
+    constexpr int QMAX = (BalShared<C, COMPACT>::SEGS * QPS + NT - 1) / NT;
+    // A page-range plan (RANGES: ngroups > 0) gives workgroup w = g * Hkv + kvh the pages
+    // [lo, hi) of the page table (relative to kv_indptr[0]), lo = nnz g / ngroups: its page list is
+    // known from the kernel arguments, so the page ids are loaded together with the descriptor
+    // block, and the ring's first pages together with the q rows.
+    int64_t lo = 0, hi = 0;
+    if constexpr (RANGES) {
+        const int64_t g = w / a.Hkv, nnz = kargs()->nnz, ng = kargs()->ngroups;
+        lo = nnz * g / ng;
+        hi = nnz * (g + 1) / ng;
+    }
+    int nseg;
+    if constexpr (!UNI) {
+        // round trip 1: the whole descriptor block (one int per thread), and the page ids of a
+        // page-range plan
+        const int32_t* desc = kargs()->desc + (size_t)w * kBalDescInts;
+        const int32_t* kvi = kargs()->kv_indices + lo;   // (pointers read from the arguments once)
+        const int dv = tid < kBalDescInts ? desc[tid] : 0;
+        int pv[PMAX];
+        const int npr = (int)(hi - lo);
+#pragma unroll
+        for (int k = 0; k < PMAX; ++k) {
+            const int i = tid + k * NT;
+            pv[k] = i < npr ? kvi[i] : 0;
+        }
+        if (tid < kBalDescInts) sd[tid] = dv;
+#pragma unroll
+        for (int k = 0; k < PMAX; ++k)
+            if (tid + k * NT < npr) pg[tid + k * NT] = pv[k];
+        __syncthreads();
+        PD_STAMP(1);
+        nseg = __builtin_amdgcn_readfirstlane(sd[0]);
+        // (uniform: every thread leaves) no segment, or not this plan's descriptor block: the
+        // workspace was written over since the upload, and nothing here is to be trusted
+        if (nseg <= 0 || nseg > BalShared<C, COMPACT>::SEGS ||
+            __builtin_amdgcn_readfirstlane(sd[1]) != kargs()->tag)
+            return;
+    } else {
+        // items w, w + W, ...: thread t builds the descriptor of the t-th (the decode_partial
+        // rule, 01_decode_attention.cu:88-97: keys [kv_start + chunk * chunk_tokens, + chunk_tokens)
+        // clipped to the sequence; an empty range writes 0 / -inf). t0 is the first key of the
+        // range, which need not start a page: keys are numbered from its page's first token.
+        nseg = min(u->per_wg, (u->n_items - w + a.W - 1) / a.W);
+        if (nseg <= 0) return;   // uniform: the host sizes the grid so that every workgroup has items
+        if (tid < nseg) {
+            const int item = w + tid * a.W;
+            const int pair = item / u->num_chunks, chunk = item - pair * u->num_chunks;
+            const int b = pair / a.Hkv, kvh = pair - b * a.Hkv;
+            const int pb = u->kv_indptr[b], np = u->kv_indptr[b + 1] - pb;
+            // (a last-page length outside [1, 16] is clamped: no key past the sequence's pages)
+            const int len = np > 0 ? (np - 1) * kPage + min(kPage, max(1, u->kv_last[b])) : 0;
+            const int kbeg = u->kv_start + chunk * u->chunk_tokens;
+            const int kend = max(kbeg, min(len, kbeg + u->chunk_tokens));
+            const int pf = kbeg / kPage;
+            int* sg = seg + tid * kSegInts;
+            sg[0] = b;
+            sg[1] = kvh;
+            sg[3] = kend > kbeg ? (kend - 1) / kPage - pf + 1 : 0;
+            sg[4] = kbeg;
+            sg[5] = kend;
+            sg[6] = pb + pf;
+            sg[7] = a.out != nullptr ? -1 : u->chunk_base + chunk;
+        }
+        __syncthreads();
+        // page-list offsets: exclusive prefix sum of the page counts
+        if (tid < nseg) {
+            int qa = 0;
+            for (int j = 0; j < tid; ++j) qa += seg[j * kSegInts + 3];
+            seg[tid * kSegInts + 2] = qa;
+        }
+        __syncthreads();
+        PD_STAMP(1);
+    }
+
+    run_segments<C, COMPACT, RANGES>(a, S, nseg);
+}
+
+// ---- page ranges found on the device (the drop-in decode_attention without a host plan) -----
+template <class C, bool COMPACT>
+struct DevShared {
+    BalShared<C, COMPACT> b;
+    int ip[kDevMaxB + 1];      // kv_indptr
+    int sc[C::NW + 1];         // block-scan scratch; sc[NW]: the current batch's first page
+};
+
+// Exclusive prefix sum of v over the workgroup's threads, in thread order, and the total. All
+// threads call it (it holds two barriers).
+template <int NW>
+__device__ __forceinline__ int block_exscan(int v, int* sc, int& total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+    }
+    if (lane == 63) sc[wave] = x;
+    __syncthreads();
+    int base = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+        const int t = sc[i];
+        base += i < wave ? t : 0;
+        tot += t;
+    }
+    __syncthreads();
+    total = tot;
+    return base + x - v;
+}
+
+// Workgroup w = g * Hkv + kvh: range g of the attended pages, kv head kvh. Thread t handles
+// sequences 4 t .. 4 t + 3 (B <= kDevMaxB). One round trip loads kv_indptr and the last-page
+// lengths; two block scans give the prefix sums of the attended pages and the index of each
+// sequence piece in the range; the pieces are then run in batches of at most SEGS segments (a
+// range of many short sequences), each batch like a host plan's workgroup (run_segments).
+template <class C, bool COMPACT>
+__device__ __forceinline__ void dev_body(const DevArgs& da, DevShared<C, COMPACT>& D, int w) {
+    constexpr int G = C::G, NW = C::NW, NT = C::NT, SEGS = BalShared<C, COMPACT>::SEGS;
+    static_assert(4 * NT >= kDevMaxB + 1, "four sequences per thread");
+    const BalArgs& a = da.d;
+    const int tid = threadIdx.x, B = a.B, Hkv = a.Hkv;
+    const int g = w / Hkv, kvh = w - g * Hkv;
+    PD_STAMP(0);
+    int ipv[4], lnv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int b = 4 * tid + k;
+        ipv[k] = b <= B ? da.kv_indptr[b] : 0;
+        lnv[k] = b < B ? da.kv_last[b] : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (4 * tid + k <= B) D.ip[4 * tid + k] = ipv[k];
+    __syncthreads();
+    PD_STAMP(1);
+    // attended pages of each sequence: keys [ks, min(len, ks + span)), from page ks / 16 (a
+    // last-page length outside [1, 16] is clamped, as in the uniform split)
+    const int64_t ks = da.kv_start, ke = ks + da.span;
+    int cnt[4], lenv[4], sum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int b = 4 * tid + k;
+        int c = 0, len = 0;
+        if (b < B) {
+            const int np = D.ip[b + 1] - D.ip[b];
+            len = np > 0 ? (np - 1) * kPage + min(kPage, max(1, lnv[k])) : 0;
+            const int64_t kend = min((int64_t)len, ke);
+            c = kend > ks ? (int)((kend - 1) / kPage - ks / kPage + 1) : 0;
+        }
+        cnt[k] = c;
+        lenv[k] = len;
+        sum += c;
+    }
+    int N = 0;
+    const int pre0 = block_exscan<NW>(sum, D.sc, N);
+    int pb[4];
+    {
+        int run = pre0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            pb[k] = run;
+            run += cnt[k];
+        }
+    }
+    if (w == 0) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (4 * tid + k <= B) da.prefix[4 * tid + k] = pb[k];
+    }
+    const int64_t NG = a.ngroups;
+    const int64_t lo = (int64_t)N * g / NG, hi = (int64_t)N * (g + 1) / NG;
+    if (lo == hi) {
+        // an empty range (fewer pages than ranges): its slots are read as empty by the merge
+        if (tid < 2 * G) a.part_lse[((size_t)2 * w + tid / G) * G + tid % G] = -INFINITY;
+        return;
+    }
+    int fl[4], nf = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        fl[k] = cnt[k] > 0 && pb[k] < hi && pb[k] + cnt[k] > lo;
+        nf += fl[k];
+    }
+    int ntot = 0;
+    const int f0 = block_exscan<NW>(nf, D.sc, ntot);
+    int* sd = D.b.sd;
+    int* seg = sd + 8;
+    for (int sb = 0; sb < ntot; sb += SEGS) {
+        const int nseg = min(SEGS, ntot - sb);
+        // the batch's page list starts at its first segment's first page
+        {
+            int fi = f0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (fl[k]) {
+                    if (fi == sb) D.sc[NW] = (int)max((int64_t)pb[k], lo);
+                    ++fi;
+                }
+        }
+        __syncthreads();
+        const int bs0 = D.sc[NW];
+        int fi = f0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (!fl[k]) continue;
+            const int si = fi++ - sb;
+            if (si < 0 || si >= nseg) continue;
+            const int b = 4 * tid + k;
+            const int64_t s0 = max((int64_t)pb[k], lo), s1 = min((int64_t)pb[k] + cnt[k], hi);
+            const int pa0 = (int)(ks / kPage + (s0 - pb[k])), pa1 = (int)(ks / kPage + (s1 - pb[k]));
+            const int kend = (int)min((int64_t)lenv[k], ke);
+            int* sg = seg + si * kSegInts;
+            sg[0] = b;
+            sg[1] = kvh;
+            sg[2] = (int)(s0 - bs0);
+            sg[3] = (int)(s1 - s0);
+            sg[4] = (int)max(ks, (int64_t)pa0 * kPage);
+            sg[5] = min(kend, pa1 * kPage);
+            sg[6] = D.ip[b] + pa0;
+            sg[7] = (s0 == pb[k] && s1 == (int64_t)pb[k] + cnt[k]) ? -1
+                    : (s0 == lo && pb[k] < lo) ? 2 * w : 2 * w + 1;
+        }
+        if (tid == 0) sd[0] = nseg;
+        __syncthreads();
+        run_segments<C, COMPACT, false>(a, D.b, nseg);
+    }
+}
+
+// Merge of the sequences split over ranges: one workgroup per row (b, q head); the prefix sums
+// written by the decode launch say which ranges hold sequence b's pages. A row of a sequence
+// with no attended key gets 0 / -inf; a sequence within one range was written by its workgroup.
+__global__ __launch_bounds__(kMergeThreads) void merge_ranges_kernel(DevMergeArgs a) {
+    const int row = blockIdx.x, b = row / a.Hq, hq = row - b * a.Hq;
+    const int kvh = hq / a.G, hh = hq - kvh * a.G;
+    const int64_t pb = a.prefix[b], pe = a.prefix[b + 1], N = a.prefix[a.B];
+    MState st{-INFINITY, 0.f, make_float4(0.f, 0.f, 0.f, 0.f)};
+    if (pe > pb) {
+        const int64_t NG = a.ngroups;
+        const int64_t g0 = ((pb + 1) * NG - 1) / N, g1 = (pe * NG - 1) / N;
+        if (g0 == g1) return;
+        const size_t i0 = ((size_t)(g0 * a.Hkv + kvh) * 2 + 1) * a.G + hh;       // slot 2 w + 1 of g0
+        const size_t i1 = ((size_t)((g0 + 1) * a.Hkv + kvh) * 2) * a.G + hh;     // slot 2 w of g0 + 1
+        const MSrc A{a.part_lse + i0, a.part_o + i0 * kHeadDim, 1, 1};
+        const MSrc Bs{a.part_lse + i1, a.part_o + i1 * kHeadDim, (size_t)2 * a.Hkv * a.G, (int)(g1 - g0)};
+        st = merge_lanes(A, Bs, [](int) { return true; });
+    } else {
+        // (the fold leaves the empty state: out 0, lse -inf)
+        const MSrc E{a.part_lse, a.part_o, 1, 0};
+        st = merge_lanes(E, E, [](int) { return true; });
+    }
+    merge_store(st, a.out + (size_t)row * kHeadDim, a.lse + row);
+}
+
 // At G = 8 the per-page VALU work is about twice G = 4's and no longer hides under the page's
 // memory time with one wave per SIMD, so the kernel uses the compact LDS layout (61 KB) and the
 // planner gives it two workgroups per CU: the two waves on each SIMD overlap one's arithmetic with
@@ -1051,6 +1249,14 @@ template <class C>
 __global__ __launch_bounds__(C::NT) void decode_uniform_kernel(UniArgs u) {
     __shared__ BalShared<C, (C::G > 4)> S;   // G = 8: compact, two workgroups per CU (as above)
     balanced_body<C, true, (C::G > 4)>(u.d, S, blockIdx.x, &u);
+}
+
+// The drop-in decode_attention over page ranges found on the device (G = 8: the compact layout,
+// two workgroups per CU, as for the plan path).
+template <class C>
+__global__ __launch_bounds__(C::NT) void decode_ranges_kernel(DevArgs d) {
+    __shared__ DevShared<C, (C::G > 4)> S;
+    dev_body<C, (C::G > 4)>(d, S, blockIdx.x);
 }
 
 // The fused cascade step: blocks [0, n_dec) are the suffix decode's workgroups, the rest the
@@ -1113,6 +1319,10 @@ template <class C>
 void launch_step(const StepArgs& a, hipStream_t s) {
     if (a.d.ngroups > 0) cascade_step_kernel<C, true><<<a.n_dec + a.n_pre, C::NT, 0, s>>>(a);
     else cascade_step_kernel<C, false><<<a.n_dec + a.n_pre, C::NT, 0, s>>>(a);
+}
+template <class C>
+void launch_r(const DevArgs& a, hipStream_t s) {
+    decode_ranges_kernel<C><<<a.d.W, C::NT, 0, s>>>(a);
 }
 template <class C>
 int occ_step() { return occupancy_of(reinterpret_cast<const void*>(&cascade_step_kernel<C, true>), C::NT); }
@@ -1178,6 +1388,19 @@ hipError_t launch_merge_split(const MergeArgs& a, int n_entries, hipStream_t s) 
     if (n_entries <= 0) return hipSuccess;
     if (a.cmax > 0) merge_split_kernel<true><<<n_entries * a.G, kMergeThreads, 0, s>>>(a);
     else merge_split_kernel<false><<<n_entries * a.G, kMergeThreads, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_ranges(const DevArgs& a, int G, hipStream_t s) {
+    if (G != 1 && G != 2 && G != 4 && G != 8) return hipErrorInvalidValue;
+    if (a.d.W <= 0) return hipSuccess;
+    PD_DISPATCH(BalCfg, G, launch_r, a, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_merge_ranges(const DevMergeArgs& a, hipStream_t s) {
+    if (a.B <= 0) return hipSuccess;
+    merge_ranges_kernel<<<a.B * a.Hq, kMergeThreads, 0, s>>>(a);
     return hipGetLastError();
 }
 

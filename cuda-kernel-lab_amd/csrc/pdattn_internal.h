@@ -83,6 +83,38 @@ struct UniArgs {
     int kv_start, chunk_tokens, num_chunks, chunk_base, n_items, per_wg;
 };
 
+// The drop-in decode_attention with the work cut into equal page ranges on the device, with no
+// host plan (pdattn_decode_attention_balanced). Sequence b attends keys [kv_start, kv_start + span)
+// of its own (span = num_chunks * chunk_tokens, the reference's clip), i.e. c_b of its pages;
+// the attended pages of all sequences, in page-table order, are cut into d.ngroups equal ranges,
+// and workgroup g * Hkv + kvh takes range g for kv head kvh: every workgroup loads kv_indptr and
+// kv_last_page_len, forms the prefix sums of c_b itself and cuts its range into segments (one per
+// sequence piece, at most B <= kDevMaxB sequences). A piece that is a whole sequence writes the
+// final out / lse; the pieces of a split sequence write partial slot 2 w (the piece that starts
+// the range, the sequence having started before it) or 2 w + 1 (the piece that ends the range,
+// the sequence going on after it), slot-major [2 W, G, 128]. A workgroup with an empty range
+// marks both its slots empty (lse = -inf). Workgroup 0 writes the prefix sums for the merge.
+constexpr int kDevMaxB = 1023;
+struct DevArgs {
+    BalArgs         d;            // d.kv_indices not offset; d.ngroups ranges; d.part_o / d.part_lse the slots
+    const int32_t*  kv_indptr;
+    const int32_t*  kv_last;
+    int32_t*        prefix;       // [B + 1]: attended pages of the sequences before b
+    int64_t         span;         // keys [kv_start, kv_start + span) of each sequence
+    int             kv_start;
+};
+
+// The merge after it: one workgroup per row (b, q head). A sequence whose pages lie in ranges
+// g0 < g1 merges range g0's slot 2 w + 1 and the slots 2 w of ranges g0 + 1 .. g1, in that order.
+struct DevMergeArgs {
+    const int32_t*  prefix;
+    const float*    part_o;
+    const float*    part_lse;
+    _Float16*       out;
+    float*          lse;
+    int B, Hq, Hkv, G, ngroups;
+};
+
 // Merge of split pairs (and of every pair when extra partials are given). `list` starts with a
 // header {tag, n_entries, cmax, 0}; entry e (at list[4 + 4 e]) is {b, kvh, slot0, nc}: the
 // nc >= 0 partial slots slot0 .. slot0 + nc - 1 of the pair, in order, then the n_extra extra
@@ -154,6 +186,8 @@ hipError_t launch_merge_states(const float* part_o, const float* part_lse, _Floa
 hipError_t launch_decode_balanced(const BalArgs& a, int G, hipStream_t s);
 hipError_t launch_decode_uniform(const UniArgs& a, int G, hipStream_t s);
 hipError_t launch_merge_split(const MergeArgs& a, int n_entries, hipStream_t s);
+hipError_t launch_decode_ranges(const DevArgs& a, int G, hipStream_t s);
+hipError_t launch_merge_ranges(const DevMergeArgs& a, hipStream_t s);
 hipError_t launch_fill_i32(int32_t* p, int32_t value, size_t n, hipStream_t s);
 hipError_t launch_cascade_prefix(const PrefixArgs& a, int G, int qtiles, hipStream_t s);
 hipError_t launch_cascade_step(const StepArgs& a, int G, hipStream_t s);

@@ -38,7 +38,8 @@ EXPORTS = [
     "pdattn_check_page_table",
     "pdattn_plan_chunks", "pdattn_decode_partial", "pdattn_merge_states",
     "pdattn_decode_workspace_size", "pdattn_workspace_partials", "pdattn_decode_attention",
-    "pdattn_decode_attention_noalloc",
+    "pdattn_decode_attention_noalloc", "pdattn_decode_attention_balanced",
+    "pdattn_decode_balanced_workspace_size",
     "pdattn_plan_create", "pdattn_plan_get_info", "pdattn_plan_workspace_size",
     "pdattn_plan_get_schedule", "pdattn_plan_upload", "pdattn_plan_run", "pdattn_plan_run_part",
     "pdattn_plan_destroy",
@@ -147,6 +148,9 @@ def lib():
         "pdattn_decode_attention": ([ctypes.POINTER(DecodeParams), I, I, P, P,
                                      ctypes.POINTER(Workspace), P], I),
         "pdattn_decode_attention_noalloc": ([ctypes.POINTER(DecodeParams), I, I, P, P, P], I),
+        "pdattn_decode_attention_balanced": ([ctypes.POINTER(DecodeParams), I, I, P, P,
+                                              ctypes.POINTER(Workspace), P], I),
+        "pdattn_decode_balanced_workspace_size": ([ctypes.POINTER(DecodeParams), I], S),
         "pdattn_plan_create": ([P, P, I, I, I, I, I, ctypes.POINTER(P)], I),
         "pdattn_plan_get_info": ([P, ctypes.POINTER(PlanInfo)], I),
         "pdattn_plan_get_schedule": ([P, P, S], I),
@@ -277,6 +281,18 @@ def decode_attention_noalloc(p: DecodeParams, G: int, out, lse, stream=None, var
     own device array (no allocation, no workspace)."""
     _check(lib().pdattn_decode_attention_noalloc(ctypes.byref(p), G, variant, ptr(out), ptr(lse),
                                                  stream_ptr(stream)), "pdattn_decode_attention_noalloc")
+
+
+def decode_attention_balanced(p: DecodeParams, G: int, out, lse, ws: Workspace, stream=None,
+                              variant: int = 0):
+    """pdattn_decode_attention_balanced: decode_attention's arguments, page ranges on the device."""
+    _check(lib().pdattn_decode_attention_balanced(ctypes.byref(p), G, variant, ptr(out), ptr(lse),
+                                                  ctypes.byref(ws), stream_ptr(stream)),
+           "pdattn_decode_attention_balanced")
+
+
+def decode_balanced_workspace_size(p: DecodeParams, G: int) -> int:
+    return int(lib().pdattn_decode_balanced_workspace_size(ctypes.byref(p), G))
 
 
 def workspace_reserve(ws: Workspace, nbytes: int):

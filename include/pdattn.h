@@ -149,6 +149,25 @@ int pdattn_decode_attention(const pdattn_decode_params* p, int G, int variant, v
 int pdattn_decode_attention_noalloc(const pdattn_decode_params* p, int G, int variant, void* out,
                                     float* lse, void* stream);
 
+/* decode_attention with the reference-shaped arguments and no host plan, balanced on the device:
+ * the pages that each sequence attends (keys [kv_start, kv_start + num_chunks * chunk_tokens),
+ * the keys the reference's chunks cover, clipped to the sequence), taken in page-table order over
+ * all sequences, are cut into equal ranges, one workgroup per CU and kv head, and every workgroup
+ * finds its range from the device kv_indptr / kv_last_page_len itself (prefix sums of the page
+ * counts). Sequences of very different lengths are then balanced as by the plan path, where the
+ * uniform chunks of pdattn_decode_attention (sized by the longest sequence) leave workgroups
+ * idle. A sequence inside one range is written by its workgroup; the pieces of one cut by range
+ * boundaries are merged by a second launch, in page order (bitwise deterministic). chunk_base,
+ * part_stride, part_o and part_lse of `p` are not used: the partial states live in `ws`, grown
+ * like decode_attention's when library-owned (pdattn_decode_balanced_workspace_size bytes). More
+ * than 1023 sequences run as pdattn_decode_attention. No counterpart in the reference: it is the
+ * uneven chunking the reference names as its next step (README.md:54), behind decode_attention's
+ * arguments (01_decode_attention.cu:316-331). */
+int pdattn_decode_attention_balanced(const pdattn_decode_params* p, int G, int variant, void* out,
+                                     float* lse, pdattn_workspace* ws, void* stream);
+/* Workspace bytes pdattn_decode_attention_balanced needs for `p` (0 on an invalid `p`). */
+size_t pdattn_decode_balanced_workspace_size(const pdattn_decode_params* p, int G);
+
 /* ---- balanced path (plan / run) ---------------------------------------------------------- */
 /* The MI355X path for decode_attention. The planner works on the host, from the host copy of the
  * page table, the way FlashInfer's plan() does. It cuts the pages of all sequences, taken in

@@ -62,6 +62,22 @@ def run_uniform(db: DeviceBatch, force_chunks: int = 0):
     return o, l, nc
 
 
+def run_balanced(db: DeviceBatch, force_chunks: int = 0, kv_start: int = 0, chunks=None):
+    """decode_attention_balanced (the reference-shaped arguments, page ranges found on the
+    device) with plan_chunks' chunking, or an explicit (num_chunks, chunk_tokens)."""
+    bt = db.bt
+    nc, ct = chunks if chunks else pdattn.plan_chunks(bt.G, bt.B, bt.Hkv, max(bt.max_len - kv_start, 0),
+                                                      force_chunks)
+    p = db.params(nc, ct, kv_start)
+    ws = pdattn.Workspace()
+    try:
+        pdattn.decode_attention_balanced(p, bt.G, db.out, db.lse, ws)
+        o, l = db.results()
+    finally:
+        pdattn.workspace_release(ws)
+    return o, l
+
+
 def run_plan(db: DeviceBatch, force_workgroups: int = 0):
     bt = db.bt
     plan = pdattn.Plan(bt.indptr, bt.last, bt.B, bt.Hq, bt.Hkv, force_workgroups)

@@ -79,6 +79,20 @@ def test_poisoned_tails_uniform(force):
     check_lse(l, rl, tag=f"poisoned uniform chunks={nc}")
 
 
+@pytest.mark.parametrize("kv_start", [0, 5, 21])
+def test_poisoned_tails_balanced_on_device(kv_start):
+    """decode_attention_balanced (page ranges found on the device) with NaN / Inf in every slot
+    it must not read: the last pages' tails and the slots before kv_start."""
+    import _gpu
+    print(f"[case] poisoned tails, device ranges kv_start={kv_start}", flush=True)
+    bt = inputs.make_batch(POISON_LENS, 32, 8, seed=34)
+    ro, rl = _ref(bt, kv_start=kv_start)
+    _poison(bt, kv_start)
+    o, l = _gpu.run_balanced(_gpu.DeviceBatch(bt), kv_start=kv_start)
+    check_out(o, ro, tag=f"poisoned device ranges kv_start={kv_start}")
+    check_lse(l, rl, tag=f"poisoned device ranges kv_start={kv_start}")
+
+
 @pytest.mark.parametrize("kv_start,chunk_tokens", [(5, 40), (21, 64), (16, 48)])
 def test_poisoned_before_kv_start(kv_start, chunk_tokens):
     """Partials with kv_start inside a page: the slots before it hold NaN / Inf."""
