@@ -143,6 +143,21 @@ def uniform_runner(bt, t, stream, force_chunks=0):
     return fn, (p, ws), nc
 
 
+def balanced_runner(bt, t, stream):
+    """decode_attention_balanced: decode_attention's arguments (plan_chunks' chunking), the pages
+    cut into equal ranges on the device, with no host plan."""
+    import pdattn
+    nc, ct = pdattn.plan_chunks(bt.G, bt.B, bt.Hkv, bt.max_len)
+    p = pdattn.make_params(t["q"], t["k"], t["v"], t["indptr"], t["indices"], t["last"],
+                           bt.B, bt.Hq, bt.Hkv, nc, ct)
+    ws = pdattn.Workspace()
+    pdattn.workspace_reserve(ws, pdattn.decode_balanced_workspace_size(p, bt.G))
+
+    def fn():
+        pdattn.decode_attention_balanced(p, bt.G, t["out"], t["lse"], ws, stream)
+    return fn, (p, ws)
+
+
 ROT_BYTES = 1 << 30
 COPY_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_balanced_1x32k_traffic.md")
@@ -305,6 +320,10 @@ def decode_workload(timer, lens, args, with_uniform, seed=11, nosplit=False):
         fn_ns, k_ns, nc1 = uniform_runner(bt, t, s, force_chunks=1)
         fns.append(fn_ns)
         keep.append(k_ns)
+    if with_uniform:
+        fn_bd, k_bd = balanced_runner(bt, t, s)
+        fns.append(fn_bd)
+        keep.append(k_bd)
     times = timer.run(fns, args.steps, args.warmup, rounds=3)
     nbytes = bt.algorithmic_bytes()
     ms = statistics.median(times[0])
@@ -322,8 +341,14 @@ def decode_workload(timer, lens, args, with_uniform, seed=11, nosplit=False):
         mu = statistics.median(times[1])
         r["uniform"] = {"us_per_step": round(mu * 1e3, 2), "chunks": nc,
                         "GB/s": round(nbytes / (mu * 1e-3) / 1e9, 1)}
+    if with_uniform:
+        mb = statistics.median(times[-1])
+        r["balanced"] = {"us_per_step": round(mb * 1e3, 2), "GB/s": round(nbytes / (mb * 1e-3) / 1e9, 1),
+                         "vs_plan_run": round(mb / ms, 4),
+                         "path": "decode_attention_balanced: decode_attention's arguments, page ranges "
+                                 "found on the device (no host plan)"}
     if nosplit:
-        mn = statistics.median(times[-1])
+        mn = statistics.median(times[2 if with_uniform else 1])
         r["no_split"] = {"us_per_step": round(mn * 1e3, 2), "chunks": nc1,
                          "items": nc1 * bt.B * bt.Hkv, "GB/s": round(nbytes / (mn * 1e-3) / 1e9, 1),
                          "path": "decode_attention, force_chunks = 1"}
@@ -347,8 +372,8 @@ def decode_leg(timer, lens, args, ceil, seed=11, reference=None):
            "decode_kernel_us": round(h["decode_kernel_us"], 2),
            "merge_kernel_us": round(h["merge_kernel_us"], 2),
            "decode_kernel_pct_of_peak": round(100 * gbs(h["bytes"], h["decode_kernel_us"] * 1e-6) / PEAK_GBS, 1),
-           "uniform_path": h["uniform"], "no_split": h["no_split"]}
-    for leg in (out["uniform_path"], out["no_split"]):
+           "uniform_path": h["uniform"], "no_split": h["no_split"], "balanced_path": h["balanced"]}
+    for leg in (out["uniform_path"], out["no_split"], out["balanced_path"]):
         leg["pct_of_peak"] = round(100 * leg["GB/s"] / PEAK_GBS, 1)
         leg["pct_of_ceiling"] = round(100 * leg["GB/s"] / ceil, 1)
     if reference:
@@ -845,6 +870,8 @@ def main():
     )
     if "uniform" in h:
         result["uniform_path"] = h["uniform"]
+    if "balanced" in h:
+        result["balanced_path"] = h["balanced"]
     if "no_split" in h:
         result["no_split"] = h["no_split"]
     if full:
@@ -860,7 +887,7 @@ def main():
             "what": "stream_read over the workload's algorithmic bytes in one launch, back to back "
                     "over rotated buffers (>= 1 GiB); kernel_frac = its time / the decode step's"}
         result["reference_published"] = REF_DECODE["1x32K"]
-        for sub in (result.get("no_split"), result.get("uniform_path")):
+        for sub in (result.get("no_split"), result.get("uniform_path"), result.get("balanced_path")):
             if sub:
                 sub["pct_of_peak"] = round(100 * sub["GB/s"] / PEAK_GBS, 1)
                 sub["pct_of_ceiling"] = round(100 * sub["GB/s"] / ceil, 1)

@@ -85,6 +85,22 @@ __device__ __forceinline__ float row_sum(float v) {
     return v;
 }
 
+// row_sum of N independent values, one DPP step at a time across all of them (the same sums,
+// bitwise: each value goes through the same sequence of adds).
+template <int LPR, int N>
+__device__ __forceinline__ void row_sum_all(float* v) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] += dpp<0xB1>(v[j]);
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] += dpp<0x4E>(v[j]);
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] += dpp<0x141>(v[j]);
+    if constexpr (LPR == 16) {
+#pragma unroll
+        for (int j = 0; j < N; ++j) v[j] += dpp<0x140>(v[j]);
+    }
+}
+
 // Combine of the 64/LPR row groups of a wave (lanes LPR apart hold the same head dims), leaving
 // the result in every lane: row_ror:8 pairs the two groups of a 16-lane row (LPR = 8), then
 // v_permlane16_swap / v_permlane32_swap pair whole 16-lane rows, all in the VALU. After
@@ -204,11 +220,12 @@ __device__ __forceinline__ void page_step(WaveState<C>& st, PageRegs<C>& pr,
             }
         }
     }
+    // Scores: the lane's partial dot products of every (row, head) first, then each DPP step of
+    // the row sums across all of them, so that every dependent DPP add has RG * G - 1 independent
+    // instructions in front of it instead of a hazard stall (s_nop).
     float x[g::RG][G];
 #pragma unroll
-    for (int i = 0; i < g::RG; ++i) {
-        const int tok = tok_r + i * g::RPI;
-        const bool ok = tok >= tb && tok < te;
+    for (int i = 0; i < g::RG; ++i)
 #pragma unroll
         for (int h = 0; h < G; ++h) {
             float acc = 0.f;
@@ -219,9 +236,15 @@ __device__ __forceinline__ void page_step(WaveState<C>& st, PageRegs<C>& pr,
                     acc = __builtin_amdgcn_fdot2(qv[h][kk][e],
                                                  as_h2(pr.k[i][kk][e]), acc,
                                                  false);
-            acc = row_sum<g::LPR>(acc);
-            x[i][h] = ok ? acc * scale2 : -INFINITY;
+            x[i][h] = acc;
         }
+    row_sum_all<g::LPR, g::RG * G>(&x[0][0]);
+#pragma unroll
+    for (int i = 0; i < g::RG; ++i) {
+        const int tok = tok_r + i * g::RPI;
+        const bool ok = tok >= tb && tok < te;
+#pragma unroll
+        for (int h = 0; h < G; ++h) x[i][h] = ok ? x[i][h] * scale2 : -INFINITY;
     }
     float mn[G];
     bool grow = false;
@@ -1134,11 +1157,35 @@ __device__ __forceinline__ void dev_body(const DevArgs& da, DevShared<C, COMPACT
         lenv[k] = len;
         sum += c;
     }
-    int N = 0;
-    const int pre0 = block_exscan<NW>(sum, D.sc, N);
-    int pb[4];
-    {
-        int run = pre0;
+    // The common case: keys from 0 and no sequence cut short by the span. The attended pages of
+    // sequence b are then all its pages, the prefix sums are kv_indptr[b] - kv_indptr[0], and a
+    // range's page ids are contiguous in kv_indices: they are loaded at once (the segments are
+    // built while they are in flight) and the segments run as a host page-range plan's do.
+    int clipped = ks > 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int b = 4 * tid + k;
+        if (b < B && cnt[k] != D.ip[b + 1] - D.ip[b]) clipped = 1;
+    }
+    // (an LDS flag: HIP's __syncthreads_or reads the block size from the dispatch packet, two
+    // dependent global loads)
+    if (tid == 0) D.sc[NW] = 0;
+    __syncthreads();
+    if (clipped) D.sc[NW] = 1;
+    __syncthreads();
+    const bool fast = D.sc[NW] == 0;
+    __syncthreads();   // (sc is reused below)
+    int N = 0, pb[4];
+    if (fast) {
+        const int ip0 = D.ip[0];
+        N = D.ip[B] - ip0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int b = 4 * tid + k;
+            pb[k] = b <= B ? D.ip[b] - ip0 : N;
+        }
+    } else {
+        int run = block_exscan<NW>(sum, D.sc, N);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             pb[k] = run;
@@ -1157,6 +1204,14 @@ __device__ __forceinline__ void dev_body(const DevArgs& da, DevShared<C, COMPACT
         if (tid < 2 * G) a.part_lse[((size_t)2 * w + tid / G) * G + tid % G] = -INFINITY;
         return;
     }
+    constexpr int PMAX = kRangeMax / NT;
+    int pv[PMAX];
+    if (fast) {
+        const int32_t* kvi = kargs()->kv_indices + D.ip[0] + lo;
+        const int npr = (int)(hi - lo);
+#pragma unroll
+        for (int k = 0; k < PMAX; ++k) pv[k] = tid + k * NT < npr ? kvi[tid + k * NT] : 0;
+    }
     int fl[4], nf = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -1167,15 +1222,21 @@ __device__ __forceinline__ void dev_body(const DevArgs& da, DevShared<C, COMPACT
     const int f0 = block_exscan<NW>(nf, D.sc, ntot);
     int* sd = D.b.sd;
     int* seg = sd + 8;
-    for (int sb = 0; sb < ntot; sb += SEGS) {
-        const int nseg = min(SEGS, ntot - sb);
-        // the batch's page list starts at its first segment's first page
+    if (fast) {
+        // the range's page list (the batch loop's first barrier publishes it)
+#pragma unroll
+        for (int k = 0; k < PMAX; ++k)
+            if (tid + k * NT < hi - lo) D.b.pg[tid + k * NT] = pv[k];
+    }
+    // Descriptors of segments [sb, sb + nseg) (the batch's page list starts at its first
+    // segment's first page; the fast path's at the range's first page, its list being the range).
+    auto describe = [&](int sb, int nseg) {
         {
             int fi = f0;
 #pragma unroll
             for (int k = 0; k < 4; ++k)
                 if (fl[k]) {
-                    if (fi == sb) D.sc[NW] = (int)max((int64_t)pb[k], lo);
+                    if (fi == sb) D.sc[NW] = fast ? (int)lo : (int)max((int64_t)pb[k], lo);
                     ++fi;
                 }
         }
@@ -1204,6 +1265,19 @@ __device__ __forceinline__ void dev_body(const DevArgs& da, DevShared<C, COMPACT
         }
         if (tid == 0) sd[0] = nseg;
         __syncthreads();
+    };
+    // The common case, every piece of the range in one batch: the segment runner is the last
+    // thing the workgroup does, so none of the state above stays live through its page loop
+    // (which then compiles to the plan path's schedule: measured 7% slower streaming otherwise).
+    if (ntot <= SEGS) {
+        describe(0, ntot);
+        if (fast) run_segments<C, COMPACT, true>(a, D.b, ntot);
+        else run_segments<C, COMPACT, false>(a, D.b, ntot);
+        return;
+    }
+    for (int sb = 0; sb < ntot; sb += SEGS) {
+        const int nseg = min(SEGS, ntot - sb);
+        describe(sb, nseg);
         run_segments<C, COMPACT, false>(a, D.b, nseg);
     }
 }

@@ -248,6 +248,16 @@ void decode_case(const char* name, const std::vector<int>& lens, int Hq, int Hkv
             std::snprintf(tag, sizeof tag, "%s decode_attention_noalloc chunks=%d", name, nc);
             check(tag, b, db);
         }
+        // the same arguments, the pages cut into equal ranges on the device, in a workspace the
+        // caller sized with pdattn_decode_balanced_workspace_size
+        const size_t bb = pdattn_decode_balanced_workspace_size(&p, G);
+        void* wb = nullptr;
+        HIP_OK(hipMalloc(&wb, bb > 0 ? bb : 256));
+        pdattn_workspace wsb{wb, bb, 0};
+        PD_OK(pdattn_decode_attention_balanced(&p, G, 2, db.out, db.lse, &wsb, nullptr));
+        std::snprintf(tag, sizeof tag, "%s decode_attention_balanced chunks=%d", name, nc);
+        check(tag, b, db);
+        HIP_OK(hipFree(wb));
     }
     pdattn_plan* plan = nullptr;
     PD_OK(pdattn_plan_create(b.indptr.data(), b.last.data(), b.B, Hq, Hkv, 0, 0, &plan));
