@@ -1086,6 +1086,7 @@ template <class C, bool COMPACT>
 struct DevShared {
     BalShared<C, COMPACT> b;
     int ip[kDevMaxB + 1];      // kv_indptr
+    int wx[2 * C::NW];         // per-wave piece counts and clip flags of the common-case guess
     int sc[C::NW + 1];         // block-scan scratch; sc[NW]: the current batch's first page
 };
 
@@ -1116,132 +1117,137 @@ __device__ __forceinline__ int block_exscan(int v, int* sc, int& total) {
 
 // Workgroup w = g * Hkv + kvh: range g of the attended pages, kv head kvh. Thread t handles
 // sequences 4 t .. 4 t + 3 (B <= kDevMaxB). One round trip loads kv_indptr and the last-page
-// lengths; two block scans give the prefix sums of the attended pages and the index of each
-// sequence piece in the range; the pieces are then run in batches of at most SEGS segments (a
-// range of many short sequences), each batch like a host plan's workgroup (run_segments).
+// lengths. In the common case (keys from 0, no sequence cut short by the span) the attended pages
+// of sequence b are all its pages, their prefix sums are kv_indptr[b] - kv_indptr[0], and a range's
+// page ids are contiguous in kv_indices: that case is assumed at once, its page ids are loaded
+// while one barrier settles whether it holds, and its pieces run as a host page-range plan's do.
+// Otherwise two block scans give the prefix sums of the attended pages and the index of each
+// sequence piece in the range, and the pieces run in batches of at most SEGS segments (a range of
+// many short sequences), each batch like a host plan's workgroup (run_segments).
 template <class C, bool COMPACT>
 __device__ __forceinline__ void dev_body(const DevArgs& da, DevShared<C, COMPACT>& D, int w) {
     constexpr int G = C::G, NW = C::NW, NT = C::NT, SEGS = BalShared<C, COMPACT>::SEGS;
+    constexpr int PMAX = kRangeMax / NT;
     static_assert(4 * NT >= kDevMaxB + 1, "four sequences per thread");
     const BalArgs& a = da.d;
-    const int tid = threadIdx.x, B = a.B, Hkv = a.Hkv;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, B = a.B, Hkv = a.Hkv;
     const int g = w / Hkv, kvh = w - g * Hkv;
+    const int64_t NG = a.ngroups;
     PD_STAMP(0);
+    // (unconditional loads at clamped indices, B >= 1: a conditional load per element would be
+    // waited for before the next is issued)
     int ipv[4], lnv[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int b = 4 * tid + k;
-        ipv[k] = b <= B ? da.kv_indptr[b] : 0;
-        lnv[k] = b < B ? da.kv_last[b] : 0;
+        ipv[k] = da.kv_indptr[min(b, B)];
+        lnv[k] = da.kv_last[min(b, B - 1)];
     }
 #pragma unroll
     for (int k = 0; k < 4; ++k)
         if (4 * tid + k <= B) D.ip[4 * tid + k] = ipv[k];
     __syncthreads();
     PD_STAMP(1);
+    // (32-bit arithmetic from here on: page positions are int32, and a sequence's keys fit an int;
+    // wave64 integer work costs four cycles an instruction, and 64-bit work twice that)
+    const int ks = da.kv_start;   // >= 0
+    const int ke = (int)min((int64_t)ks + da.span, (int64_t)INT_MAX);
+    // The common-case guess (uniform: every thread takes the same branches on it). Its page ids
+    // [ip0 + lo, ip0 + hi) lie in [ip0, kv_indptr[B]), entries of the page table whatever the
+    // outcome; a range of more than kRangeMax pages (the guess being wrong) loads only the first.
+    // They are loaded first, while the rest is worked out.
+    const int ip0 = __builtin_amdgcn_readfirstlane(D.ip[0]);
+    const int ipB = __builtin_amdgcn_readfirstlane(D.ip[B]);
+    const bool guess = ks == 0 && ip0 >= 0 && ipB >= ip0;
+    int N = guess ? ipB - ip0 : 0;
+    int lo = (int)((int64_t)N * g / NG), hi = (int)((int64_t)N * (g + 1) / NG);
+    // (branch-free loads at indices clamped into the range, or of kv_indptr[0] with no range to
+    // load: the waits for the loads before them then count exactly, and none waits for these)
+    int pv[PMAX];
+    {
+        const bool ok = guess && hi > lo;
+        const int32_t* kvi = ok ? kargs()->kv_indices + ip0 + lo : da.kv_indptr;
+        const int last = ok ? hi - lo - 1 : 0;
+#pragma unroll
+        for (int k = 0; k < PMAX; ++k) pv[k] = kvi[min(tid + k * NT, last)];
+    }
     // attended pages of each sequence: keys [ks, min(len, ks + span)), from page ks / 16 (a
     // last-page length outside [1, 16] is clamped, as in the uniform split)
-    const int64_t ks = da.kv_start, ke = ks + da.span;
-    int cnt[4], lenv[4], sum = 0;
+    const int ipn = D.ip[min(4 * tid + 4, B)];
+    int cnt[4], lenv[4], pb[4], sum = 0, clipped = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int b = 4 * tid + k;
-        int c = 0, len = 0;
-        if (b < B) {
-            const int np = D.ip[b + 1] - D.ip[b];
-            len = np > 0 ? (np - 1) * kPage + min(kPage, max(1, lnv[k])) : 0;
-            const int64_t kend = min((int64_t)len, ke);
-            c = kend > ks ? (int)((kend - 1) / kPage - ks / kPage + 1) : 0;
-        }
+        const int np = b < B ? (k < 3 ? ipv[k + 1] : ipn) - ipv[k] : 0;
+        const int len = np > 0 ? (np - 1) * kPage + min(kPage, max(1, lnv[k])) : 0;
+        const int kend = min(len, ke);
+        const int c = kend > ks ? (int)((uint32_t)(kend - 1) / kPage) - ks / kPage + 1 : 0;
+        clipped |= c != np;
         cnt[k] = c;
         lenv[k] = len;
+        pb[k] = b <= B ? ipv[k] - ip0 : N;
         sum += c;
     }
-    // The common case: keys from 0 and no sequence cut short by the span. The attended pages of
-    // sequence b are then all its pages, the prefix sums are kv_indptr[b] - kv_indptr[0], and a
-    // range's page ids are contiguous in kv_indices: they are loaded at once (the segments are
-    // built while they are in flight) and the segments run as a host page-range plan's do.
-    int clipped = ks > 0;
+    // one barrier: the guess's per-wave piece counts and clip flags. Piece k of each thread is one
+    // bit of a ballot, so the wave's exclusive prefix is four masked popcounts.
+    int fl[4], nf = 0, x = 0, wn = 0;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        const int b = 4 * tid + k;
-        if (b < B && cnt[k] != D.ip[b + 1] - D.ip[b]) clipped = 1;
+        fl[k] = cnt[k] > 0 && pb[k] < hi && pb[k] + cnt[k] > lo;
+        nf += fl[k];
+        const uint64_t m = __builtin_amdgcn_ballot_w64(fl[k] != 0);
+        x += __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+        wn += __builtin_popcountll(m);
     }
-    // (an LDS flag: HIP's __syncthreads_or reads the block size from the dispatch packet, two
-    // dependent global loads)
-    if (tid == 0) D.sc[NW] = 0;
+    const bool wclip = __builtin_amdgcn_ballot_w64(clipped != 0) != 0;
+    if (lane == 0) {
+        D.wx[wave] = wn;
+        D.wx[NW + wave] = wclip;
+    }
     __syncthreads();
-    if (clipped) D.sc[NW] = 1;
-    __syncthreads();
-    const bool fast = D.sc[NW] == 0;
-    __syncthreads();   // (sc is reused below)
-    int N = 0, pb[4];
-    if (fast) {
-        const int ip0 = D.ip[0];
-        N = D.ip[B] - ip0;
+    PD_STAMP(28);
+    int f0 = x, ntot = 0, anyclip = 0;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int b = 4 * tid + k;
-            pb[k] = b <= B ? D.ip[b] - ip0 : N;
-        }
-    } else {
+    for (int i = 0; i < NW; ++i) {
+        const int t = D.wx[i];
+        f0 += i < wave ? t : 0;
+        ntot += t;
+        anyclip |= D.wx[NW + i];
+    }
+    const bool fast = guess && !anyclip;
+    if (!fast) {
+        // prefix sums of the attended pages, then the pieces of the range
         int run = block_exscan<NW>(sum, D.sc, N);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             pb[k] = run;
             run += cnt[k];
         }
+        lo = (int)((int64_t)N * g / NG);
+        hi = (int)((int64_t)N * (g + 1) / NG);
+        nf = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            fl[k] = cnt[k] > 0 && pb[k] < hi && pb[k] + cnt[k] > lo;
+            nf += fl[k];
+        }
+        f0 = block_exscan<NW>(nf, D.sc, ntot);
     }
     if (w == 0) {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
             if (4 * tid + k <= B) da.prefix[4 * tid + k] = pb[k];
     }
-    const int64_t NG = a.ngroups;
-    const int64_t lo = (int64_t)N * g / NG, hi = (int64_t)N * (g + 1) / NG;
     if (lo == hi) {
         // an empty range (fewer pages than ranges): its slots are read as empty by the merge
         if (tid < 2 * G) a.part_lse[((size_t)2 * w + tid / G) * G + tid % G] = -INFINITY;
         return;
     }
-    constexpr int PMAX = kRangeMax / NT;
-    int pv[PMAX];
-    if (fast) {
-        const int32_t* kvi = kargs()->kv_indices + D.ip[0] + lo;
-        const int npr = (int)(hi - lo);
-#pragma unroll
-        for (int k = 0; k < PMAX; ++k) pv[k] = tid + k * NT < npr ? kvi[tid + k * NT] : 0;
-    }
-    int fl[4], nf = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        fl[k] = cnt[k] > 0 && pb[k] < hi && pb[k] + cnt[k] > lo;
-        nf += fl[k];
-    }
-    int ntot = 0;
-    const int f0 = block_exscan<NW>(nf, D.sc, ntot);
     int* sd = D.b.sd;
     int* seg = sd + 8;
-    if (fast) {
-        // the range's page list (the batch loop's first barrier publishes it)
-#pragma unroll
-        for (int k = 0; k < PMAX; ++k)
-            if (tid + k * NT < hi - lo) D.b.pg[tid + k * NT] = pv[k];
-    }
-    // Descriptors of segments [sb, sb + nseg) (the batch's page list starts at its first
-    // segment's first page; the fast path's at the range's first page, its list being the range).
-    auto describe = [&](int sb, int nseg) {
-        {
-            int fi = f0;
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if (fl[k]) {
-                    if (fi == sb) D.sc[NW] = fast ? (int)lo : (int)max((int64_t)pb[k], lo);
-                    ++fi;
-                }
-        }
-        __syncthreads();
-        const int bs0 = D.sc[NW];
+    // Descriptors of segments [sb, sb + nseg) whose page list starts at page bs0 of the attended
+    // pages; the caller publishes them with a barrier.
+    auto describe = [&](int sb, int nseg, int bs0) {
         int fi = f0;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -1249,35 +1255,52 @@ __device__ __forceinline__ void dev_body(const DevArgs& da, DevShared<C, COMPACT
             const int si = fi++ - sb;
             if (si < 0 || si >= nseg) continue;
             const int b = 4 * tid + k;
-            const int64_t s0 = max((int64_t)pb[k], lo), s1 = min((int64_t)pb[k] + cnt[k], hi);
-            const int pa0 = (int)(ks / kPage + (s0 - pb[k])), pa1 = (int)(ks / kPage + (s1 - pb[k]));
-            const int kend = (int)min((int64_t)lenv[k], ke);
+            const int s0 = max(pb[k], lo), s1 = min(pb[k] + cnt[k], hi);
+            const int pa0 = ks / kPage + (s0 - pb[k]), pa1 = ks / kPage + (s1 - pb[k]);
+            const int kend = min(lenv[k], ke);
             int* sg = seg + si * kSegInts;
             sg[0] = b;
             sg[1] = kvh;
-            sg[2] = (int)(s0 - bs0);
-            sg[3] = (int)(s1 - s0);
-            sg[4] = (int)max(ks, (int64_t)pa0 * kPage);
+            sg[2] = s0 - bs0;
+            sg[3] = s1 - s0;
+            sg[4] = max(ks, pa0 * kPage);
             sg[5] = min(kend, pa1 * kPage);
             sg[6] = D.ip[b] + pa0;
-            sg[7] = (s0 == pb[k] && s1 == (int64_t)pb[k] + cnt[k]) ? -1
+            sg[7] = (s0 == pb[k] && s1 == pb[k] + cnt[k]) ? -1
                     : (s0 == lo && pb[k] < lo) ? 2 * w : 2 * w + 1;
         }
         if (tid == 0) sd[0] = nseg;
-        __syncthreads();
     };
-    // The common case, every piece of the range in one batch: the segment runner is the last
-    // thing the workgroup does, so none of the state above stays live through its page loop
-    // (which then compiles to the plan path's schedule: measured 7% slower streaming otherwise).
-    if (ntot <= SEGS) {
-        describe(0, ntot);
-        if (fast) run_segments<C, COMPACT, true>(a, D.b, ntot);
-        else run_segments<C, COMPACT, false>(a, D.b, ntot);
+    // The common case, every piece of the range in one batch: the range's page list is its pages,
+    // and the segment runner is the last thing the workgroup does, so none of the state above stays
+    // live through its page loop (which then compiles to the plan path's schedule: measured 7%
+    // slower streaming otherwise).
+    if (fast && ntot <= SEGS) {
+        describe(0, ntot, lo);
+#pragma unroll
+        for (int k = 0; k < PMAX; ++k)
+            if (tid + k * NT < hi - lo) D.b.pg[tid + k * NT] = pv[k];
+        __syncthreads();
+        PD_STAMP(30);
+        run_segments<C, COMPACT, true>(a, D.b, ntot);
         return;
     }
+    // Batches: each one's page list starts at its first segment's first page in the range.
     for (int sb = 0; sb < ntot; sb += SEGS) {
         const int nseg = min(SEGS, ntot - sb);
-        describe(sb, nseg);
+        {
+            int fi = f0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (fl[k]) {
+                    if (fi == sb) D.sc[NW] = max(pb[k], lo);
+                    ++fi;
+                }
+        }
+        __syncthreads();
+        const int bs0 = D.sc[NW];
+        describe(sb, nseg, bs0);
+        __syncthreads();
         run_segments<C, COMPACT, false>(a, D.b, nseg);
     }
 }
