@@ -218,21 +218,29 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
         const bool more = kb + 1 < nblk;
         if (more) gload(kb + 1);
 
-        // S^T tiles: s[tq][tk][j] = score(key 16 tk + 4 lg + j, query l16 of tile tq)
+        // S^T tiles: s[tq][tk][j] = score(key 16 tk + 4 lg + j, query l16 of tile tq). The K
+        // fragments of key tile tk + 1 are read before the MFMAs of tile tk (the scheduling fences
+        // keep them there), so the LDS latency hides under the matrix core's work.
         pf32x4 s[NT][4];
-#pragma unroll
-        for (int tk = 0; tk < 4; ++tk) {
-            pf16x8 ka[4];
+        auto kfrag = [&](int tk, pf16x8* ka) {
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
                 ka[ks] = __builtin_bit_cast(pf16x8, sm.K[buf][16 * tk + l16][(4 * ks + lg) ^ l16]);
+        };
+        pf16x8 ka[2][4];
+        kfrag(0, ka[0]);
+#pragma unroll
+        for (int tk = 0; tk < 4; ++tk) {
+            if (tk < 3) kfrag(tk + 1, ka[(tk + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int tq = 0; tq < NT; ++tq) {
                 pf32x4 c = pf32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int ks = 0; ks < 4; ++ks) c = mfma16x16x32(ka[ks], qb[tq][ks], c);
+                for (int ks = 0; ks < 4; ++ks) c = mfma16x16x32(ka[tk & 1][ks], qb[tq][ks], c);
                 s[tq][tk] = c;
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
 
         // Online softmax (base 2) per query. The scores stay unscaled: the scale is positive, so
@@ -292,26 +300,38 @@ __device__ __forceinline__ void prefix_chunk(const PrefixArgs& a, PSmem& sm, int
         // transposing reads: within a 16-lane group, lane j reads 4 dims (16 dt + 4 (j & 3) ..)
         // of key 32 kb2 + 16 h + 4 lg + (j >> 2), and lane i receives element (i & 3) of lanes
         // i / 4, i / 4 + 4, ..., i.e. dim 16 dt + i of the 4 keys.
+        // (the fragments of dim tile dt + 1 are read before the MFMAs of tile dt, as above)
+        auto vfrag = [&](int dt, int kb2) {
+            pf16x4 half[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int key = 32 * kb2 + 16 * h + 4 * lg + (l16 >> 2);
+                const int chunk = 2 * dt + ((l16 & 3) >> 1);
+                const _Float16* src =
+                    reinterpret_cast<const _Float16*>(&sm.V[buf][key][chunk ^ ((key & 7) << 1)]) + 4 * (l16 & 1);
+                half[h] = __builtin_bit_cast(pf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
+                    (__attribute__((address_space(3))) lds_f16x4*)(
+                        (__attribute__((address_space(3))) _Float16*)src)));
+            }
+            return pf16x8{half[0][0], half[0][1], half[0][2], half[0][3],
+                          half[1][0], half[1][1], half[1][2], half[1][3]};
+        };
+        pf16x8 va[2][2];
+        va[0][0] = vfrag(0, 0);
+        va[0][1] = vfrag(0, 1);
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
-#pragma unroll
-            for (int kb2 = 0; kb2 < 2; ++kb2) {
-                pf16x4 half[2];
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int key = 32 * kb2 + 16 * h + 4 * lg + (l16 >> 2);
-                    const int chunk = 2 * dt + ((l16 & 3) >> 1);
-                    const _Float16* src =
-                        reinterpret_cast<const _Float16*>(&sm.V[buf][key][chunk ^ ((key & 7) << 1)]) + 4 * (l16 & 1);
-                    half[h] = __builtin_bit_cast(pf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(
-                        (__attribute__((address_space(3))) lds_f16x4*)(
-                            (__attribute__((address_space(3))) _Float16*)src)));
-                }
-                const pf16x8 va = {half[0][0], half[0][1], half[0][2], half[0][3],
-                                   half[1][0], half[1][1], half[1][2], half[1][3]};
-#pragma unroll
-                for (int tq = 0; tq < NT; ++tq) acc[tq][dt] = mfma16x16x32(va, pb[tq][kb2], acc[tq][dt]);
+            if (dt < 7) {
+                va[(dt + 1) & 1][0] = vfrag(dt + 1, 0);
+                va[(dt + 1) & 1][1] = vfrag(dt + 1, 1);
             }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+                for (int tq = 0; tq < NT; ++tq)
+                    acc[tq][dt] = mfma16x16x32(va[dt & 1][kb2], pb[tq][kb2], acc[tq][dt]);
+            __builtin_amdgcn_sched_barrier(0);
         }
 
         if (more) lstore(buf ^ 1);
