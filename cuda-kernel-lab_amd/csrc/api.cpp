@@ -254,6 +254,7 @@ struct pdattn_plan {
     int64_t U = 0;
     int split_pairs = 0, max_contrib = 0, n_entries = 0, n_slots = 0, segments = 0;
     int cmax = 0;                     // > 0: partial slots laid out by merge entry (e * cmax + k)
+    bool pair = false;                // page-range plan run by the paired kernel (W / 2 workgroups)
     // workspace layout (bytes from the base)
     size_t off_desc = 0, off_list = 0, off_plse = 0, off_po = 0, ws_bytes = 0;
     std::vector<int32_t> host_blob;   // desc[W * kBalDescInts] followed by the merge list
@@ -312,7 +313,7 @@ namespace {
 // pages.
 int build_balanced_plan(const int32_t* indptr, const int32_t* last, int B, int Hq, int Hkv,
                         int force_wg, int chunk_pages, bool merge_all, pdattn_plan* pl,
-                        int seg_cap = 0) {
+                        int seg_cap = 0, bool pairable = false) {
     int G = 0;
     if (int st = check_heads(Hq, Hkv, &G)) return st;
     // at G = 8 the decode kernel stages q rows for at most kStepSegMax segments per workgroup
@@ -336,12 +337,16 @@ int build_balanced_plan(const int32_t* indptr, const int32_t* last, int B, int H
     // grid: one workgroup per CU (the kernel's four waves take one SIMD each; two at G = 8), never more
     // workgroups than page units; a forced size needs no device query
     int64_t W = force_wg;
+    // The paired kernel (two kv heads per workgroup, pages staged in LDS) runs a default page-range
+    // plan at G <= 4 with an even Hkv: two plan workgroups per CU, one kernel workgroup.
+    const bool pair = pairable && force_wg <= 0 && chunk_pages == 0 && !merge_all && !wide &&
+                      Hkv % 2 == 0;
     if (W <= 0) {
         DeviceFacts f;
         if (int st = device_facts(&f)) return st;
         // G = 8 (VALU-limited per page): two workgroups per CU, except for the cascade's suffix,
         // whose workgroups share the CUs with the prefix pass
-        W = (int64_t)f.cus * (wide && !merge_all ? 2 : 1);
+        W = (int64_t)f.cus * (wide && !merge_all ? 2 : 1) * (pair ? 2 : 1);
     }
     // Page-range groups, the default: the pages of all sequences, in page-table order, are cut
     // into NG = W / Hkv equal ranges, and workgroup g * Hkv + h takes range g for kv head h. The
@@ -415,6 +420,7 @@ int build_balanced_plan(const int32_t* indptr, const int32_t* last, int B, int H
         }
         pl->P = (int)((nnz + W / Hkv - 1) / (W / Hkv));   // pages per range
         pl->ngroups = (int)(W / Hkv);
+        pl->pair = pair;   // (W = NG Hkv is even: plan workgroups 2 x and 2 x + 1 share range g)
     }
     for (; !grouped;) {
         desc.assign((size_t)W * kBalDescInts, 0);
@@ -610,8 +616,11 @@ int run_plan(const pdattn_plan* pl, const void* q, const void* k, const void* v,
     float* part_o = reinterpret_cast<float*>(base + pl->off_po);
     res_written(part_lse, pl->ws_bytes - pl->off_plse, pl->id);
     res_written_outputs(out, lse, (size_t)pl->B * pl->Hq);
-    if (pl->U > 0 && decode)
-        PD_HIP(launch_decode_balanced(bal_args(pl, q, k, v, indices, sm_scale, out, lse, base), pl->G, s));
+    if (pl->U > 0 && decode) {
+        const BalArgs a = bal_args(pl, q, k, v, indices, sm_scale, out, lse, base);
+        if (pl->pair) PD_HIP(launch_decode_pair(a, pl->G, s));
+        else PD_HIP(launch_decode_balanced(a, pl->G, s));
+    }
     if (join) PD_HIP(hipStreamWaitEvent(s, join, 0));
     if (pl->n_entries && merge) {
         MergeArgs m;
@@ -1196,8 +1205,19 @@ int pdattn_plan_create(const int32_t* h_kv_indptr, const int32_t* h_kv_last_page
     *plan = nullptr;
     if (B > 0 && !h_kv_indptr) return fail(PDATTN_ERR_INVALID_ARGUMENT, "null kv_indptr");
     pdattn_plan* pl = new pdattn_plan();
-    if (int st = build_balanced_plan(h_kv_indptr, h_kv_last_page_len, B, Hq, Hkv, force_workgroups,
-                                     chunk_pages, false, pl)) {
+    int st = build_balanced_plan(h_kv_indptr, h_kv_last_page_len, B, Hq, Hkv, force_workgroups,
+                                 chunk_pages, false, pl, 0, true);
+    if (st == PDATTN_OK && pl->pair && pl->n_entries > 0) {
+        // The paired plan's ranges are half as long, so it splits this batch's sequences over
+        // twice as many workgroups: the merge's fan-in doubles, which costs more than the paired
+        // kernel gains (1x32K: 28.3 -> 30.8 us back to back). One kv head per workgroup instead.
+        free_plan_storage(pl);
+        delete pl;
+        pl = new pdattn_plan();
+        st = build_balanced_plan(h_kv_indptr, h_kv_last_page_len, B, Hq, Hkv, force_workgroups,
+                                 chunk_pages, false, pl);
+    }
+    if (st != PDATTN_OK) {
         free_plan_storage(pl);
         delete pl;
         return st;
@@ -1217,6 +1237,7 @@ int pdattn_plan_get_info(const pdattn_plan* pl, pdattn_plan_info* info) {
     info->chunk_pages = pl->P;
     info->segments = pl->segments;
     info->merge_entries = pl->n_entries;
+    info->paired = pl->pair ? 1 : 0;
     info->schedule_ints = (int)pl->host_blob.size();
     return PDATTN_OK;
 }

@@ -709,12 +709,15 @@ __device__ __forceinline__ float class_reduce(float v) {
 // raw outputs go through LDS HP heads at a time (HP = G: one pass).
 template <class C, int HP>
 __device__ __forceinline__ void flush_segment(BalSmem<C::G, C::NW * C::RPI, HP>& sm, WaveState<C>& st,
-                                              KArgPtr a, size_t row0, int slot) {
+                                              KArgPtr a, size_t row0, int slot,
+                                              int tid = threadIdx.x) {
     constexpr int G = C::G, LPR = C::LPR, NS = C::NW * C::RPI;
     // one wave computes the source weights: lane = s * G + h covers sources s + j * SL, j < J
     constexpr int SL = 64 / G, J = (NS + SL - 1) / SL;
     static_assert(NS % 4 == 0 && HP * 32 <= C::NT && G % HP == 0, "float4 passes");
-    const int tid = threadIdx.x, lane = tid & 63, c = lane % LPR;
+    // (tid: the thread's index among the C::NT threads that flush this state; every thread of the
+    // workgroup calls it, as it holds barriers)
+    const int lane = tid & 63, c = lane % LPR;
     const int src = (tid >> 6) * C::RPI + lane / LPR;
 #pragma unroll
     for (int hp = 0; hp < G / HP; ++hp) {
@@ -976,6 +979,221 @@ __device__ __forceinline__ void run_segments(const BalArgs& a, BalShared<C, COMP
     PD_STAMP(31);
 }
 
+
+// ---- the paired decode: two kv heads per workgroup, pages staged in LDS --------------------
+// A 4-wave workgroup runs two workgroups of a page-range plan, w = 2 x and 2 x + 1: kv heads
+// 2k and 2k + 1 over the same pages. Waves 0-1 serve the first head and waves 2-3 the second,
+// each pair of waves as a plan workgroup of two waves (C::NW = 2), wave i of a head taking pages
+// i, i + 2, ... of every segment. Reading the two heads' rows of a page together (1 KB of every
+// 2 KB token row at once) streams faster than one head's 256-byte rows. The page ring goes
+// through LDS instead of VGPRs: each wave moves its pages with 16-byte buffer loads straight
+// into its own LDS slots (buffer_load ... lds; lane l's pieces land at 16 l of each 1 KB, and
+// lane l reads the same bytes back), two slots per wave. The compiler makes a workgroup barrier
+// wait for every LDS-bound load in flight, so no barrier is placed while pages are in flight
+// except the flushes': q rows go straight to registers (each lane its own pieces), one segment
+// ahead, instead of through LDS.
+template <class C>
+struct PairShared {
+    static constexpr int SLOT = C::RG * C::PPL * 1024 * 2;   // one page of one head: K then V
+    BalSmem<C::G, C::NW * C::RPI> sm[2];           // flush scratch of each head's waves
+    int sd[2][kBalDescInts];                       // the two heads' descriptor blocks
+    int pg[kRangeMax];                             // the range's page ids (the same for both heads)
+    __attribute__((aligned(16))) uint8_t ring[2 * C::NW][2][SLOT];
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// One page of one head into a wave's LDS slot: lane l's pieces of row group i at
+// slot + (i PPL + kk) * 1024 + 16 l, K then V. Same offsets, resources and cache policy as the
+// VGPR ring's loads (a padding slot's zero-size resources make no memory access).
+template <class C>
+__device__ __forceinline__ void dma_page(uint8_t* slot, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+                                         uint32_t lbase, uint32_t rstride) {
+    constexpr int HALF = C::RG * C::PPL * 1024;
+#pragma unroll
+    for (int i = 0; i < C::RG; ++i)
+#pragma unroll
+        for (int kk = 0; kk < C::PPL; ++kk) {
+            const int off = (int)(lbase + i * rstride + kk * (C::LPR * 16));
+            uint8_t* d = slot + (i * C::PPL + kk) * 1024;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)d, 16, off, 0, 0, 2);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(d + HALF), 16, off, 0, 0, 2);
+        }
+}
+template <class C>
+__device__ __forceinline__ void lds_page(PageRegs<C>& pr, const uint8_t* slot, int lane) {
+    constexpr int HALF = C::RG * C::PPL * 1024;
+#pragma unroll
+    for (int i = 0; i < C::RG; ++i)
+#pragma unroll
+        for (int kk = 0; kk < C::PPL; ++kk) {
+            const uint8_t* d = slot + (i * C::PPL + kk) * 1024 + 16 * lane;
+            pr.k[i][kk] = *reinterpret_cast<const u32x4*>(d);
+            pr.v[i][kk] = *reinterpret_cast<const u32x4*>(d + HALF);
+        }
+}
+
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt at their maximum: no wait on them).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 0xF) | ((N >> 4) << 14));
+}
+// s_waitcnt lgkmcnt(0) alone.
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Workgroup x of the paired decode (page-range plans only; the plan's Hkv is even). Both heads'
+// descriptor blocks are staged; everything that decides the control flow (segments, pages,
+// tokens) is read from the first, so both halves reach every barrier together. The second head's
+// block contributes its partial slots.
+template <class C>
+__device__ __forceinline__ void pair_body(const BalArgs& a, PairShared<C>& P, int x) {
+    constexpr int G = C::G, NW = C::NW, NT2 = 2 * C::NT, LPR = C::LPR, PPL = C::PPL;
+    constexpr int PMAX = kRangeMax / NT2;
+    constexpr int DPER = (2 * kBalDescInts + NT2 - 1) / NT2;
+    constexpr int OPS = 2 * C::RG * C::PPL;       // buffer loads per page
+    static_assert(C::NBUF == 2, "two LDS slots and two register sets per wave");
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int half = wave / NW, lw = wave % NW, ltid = tid - half * C::NT;
+    const int r = lane / LPR, c = lane % LPR;
+    int* sd0 = P.sd[0];
+    int* seg0 = sd0 + 8;
+    auto fld = [&](int si, int f) { return __builtin_amdgcn_readfirstlane(seg0[si * kSegInts + f]); };
+    PD_STAMP(0);
+    // round trip 1: both descriptor blocks and the range's page ids
+    const int w0 = 2 * x;
+    const int64_t g = w0 / a.Hkv, nnz = kargs()->nnz, ng = kargs()->ngroups;
+    const int64_t lo = nnz * g / ng, hi = nnz * (g + 1) / ng;
+    {
+        const int32_t* desc = kargs()->desc + (size_t)w0 * kBalDescInts;
+        const int32_t* kvi = kargs()->kv_indices + lo;
+        int dv[DPER], pv[PMAX];
+#pragma unroll
+        for (int k = 0; k < DPER; ++k) {
+            const int i = tid + k * NT2;
+            dv[k] = i < 2 * kBalDescInts ? desc[i] : 0;
+        }
+        const int npr = (int)(hi - lo);
+#pragma unroll
+        for (int k = 0; k < PMAX; ++k) {
+            const int i = tid + k * NT2;
+            pv[k] = i < npr ? kvi[i] : 0;
+        }
+#pragma unroll
+        for (int k = 0; k < DPER; ++k) {
+            const int i = tid + k * NT2;
+            if (i < 2 * kBalDescInts) P.sd[i / kBalDescInts][i % kBalDescInts] = dv[k];
+        }
+#pragma unroll
+        for (int k = 0; k < PMAX; ++k)
+            if (tid + k * NT2 < npr) P.pg[tid + k * NT2] = pv[k];
+    }
+    __syncthreads();
+    PD_STAMP(1);
+    // (uniform: every thread leaves) either block foreign or empty, or the blocks disagree
+    const int nseg = __builtin_amdgcn_readfirstlane(sd0[0]);
+    const int kvh0 = __builtin_amdgcn_readfirstlane(nseg > 0 ? seg0[1] : 0);
+    if (nseg <= 0 || nseg > kSegMax || nseg != __builtin_amdgcn_readfirstlane(P.sd[1][0]) ||
+        __builtin_amdgcn_readfirstlane(sd0[1]) != kargs()->tag ||
+        __builtin_amdgcn_readfirstlane(P.sd[1][1]) != kargs()->tag || kvh0 < 0 || kvh0 + 1 >= a.Hkv)
+        return;
+    const int kvh = kvh0 + half;
+
+    const uint32_t page_bytes = (uint32_t)(kPage * a.Hkv * 256);
+    const uint32_t lbase = (uint32_t)(r * a.Hkv * 256 + c * 16);
+    const uint32_t rstride = (uint32_t)(C::RPI * a.Hkv * 256);
+    auto wcount = [&](int npg) { return npg > lw ? (npg - lw + NW - 1) / NW : 0; };
+    int ps = 0, pslot = 0, pcnt = 0, ppad = 0;
+    auto seek = [&]() {
+        while (ps < nseg) {
+            pcnt = wcount(fld(ps, 3));
+            ppad = (pcnt + 1) / 2 * 2;
+            if (ppad > 0) break;
+            ++ps;
+        }
+    };
+    // stream page k of this wave (padding included) goes to LDS slot k % 2 and register set k % 2
+    int nissued = 0;
+    auto issue = [&]() {
+        const uint8_t* kb = kargs()->k;
+        const uint8_t* vb = kargs()->v;
+        uint32_t nrec = 0;
+        if (ps < nseg && pslot < pcnt) {
+            const int pid = __builtin_amdgcn_readfirstlane(P.pg[fld(ps, 2) + lw + NW * pslot]);
+            const size_t off = (size_t)(uint32_t)pid * page_bytes + (size_t)kvh * 256;
+            kb += off;
+            vb += off;
+            nrec = page_bytes - (uint32_t)kvh * 256;
+        }
+        dma_page<C>(P.ring[wave][nissued & 1], page_rsrc(kb, nrec), page_rsrc(vb, nrec), lbase, rstride);
+        ++nissued;
+        if (ps < nseg && ++pslot == ppad) {
+            ++ps;
+            pslot = 0;
+            seek();
+        }
+    };
+    // this lane's q pieces of segment si (head h, piece kk: dims (kk LPR + c) 8 .. + 7)
+    auto qload = [&](int si, u32x4 (&q)[G][PPL]) {
+        const _Float16* qp = kargs()->q + ((size_t)fld(si, 0) * a.Hq + (size_t)kvh * G) * kHeadDim;
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int kk = 0; kk < PPL; ++kk)
+                q[h][kk] = *reinterpret_cast<const u32x4*>(qp + h * kHeadDim + (kk * LPR + c) * 8);
+    };
+
+    // round trip 2: the first segment's q pieces, then the first two pages of the ring
+    u32x4 qn[G][PPL];
+    qload(0, qn);
+    seek();
+    issue();
+    issue();
+    wait_vm<OPS>();            // page 0 (page 1 in flight)
+    PageRegs<C> pr[2];
+    lds_page<C>(pr[0], P.ring[wave][0], lane);
+    PD_STAMP(2);
+
+    WaveState<C> st;
+    reset_state<C>(st);
+    for (int si = 0; si < nseg; ++si) {
+        const int npg = fld(si, 3), t0 = fld(si, 4), t1 = fld(si, 5);
+        const int tbase = t0 & ~(kPage - 1);
+        f16x2 qv[G][PPL][4];
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int kk = 0; kk < PPL; ++kk)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) qv[h][kk][e] = as_h2(qn[h][kk][e]);
+        if (si + 1 < nseg) qload(si + 1, qn);   // (waited for at the next segment)
+        const int cnt = wcount(npg);
+        for (int blk = 0; blk < cnt; blk += 2) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                // page k (parity u) is in pr[u]; its slot is refilled with page k + 2 once the
+                // reads of it are done; page k + 1 (in flight since the last step) is waited for
+                // and read into pr[u ^ 1] while page k is computed
+                wait_lgkm0();
+                issue();
+                wait_vm<OPS>();
+                lds_page<C>(pr[u ^ 1], P.ring[wave][u ^ 1], lane);
+                if (blk + u < cnt)
+                    page_step<C>(st, pr[u], qv, tbase + (lw + NW * (blk + u)) * kPage, r, t0, t1,
+                                 a.scale_log2);
+            }
+            if (si == 0 && blk == 0) PD_STAMP(3);
+        }
+        if (si < 12) PD_STAMP(4 + 2 * si);
+        // this head's slot: its own block's field (the two blocks differ only in head and slot)
+        const int slot = __builtin_amdgcn_readfirstlane(P.sd[half][8 + si * kSegInts + 7]);
+        flush_segment<C, G>(P.sm[half], st, kargs(), (size_t)fld(si, 0) * a.Hq + (size_t)kvh * G, slot, ltid);
+        reset_state<C>(st);
+        if (si < 12) PD_STAMP(5 + 2 * si);
+    }
+    PD_STAMP(31);
+}
 
 // The body of one balanced-decode workgroup w (the kernel's argument block must start with the
 // BalArgs `a`, which kargs() reads).
@@ -1340,6 +1558,14 @@ __global__ __launch_bounds__(C::NT) void decode_balanced_kernel(BalArgs a) {
     balanced_body<C, false, (C::G > 4), RANGES>(a, S, blockIdx.x);
 }
 
+// The paired decode (two kv heads per 4-wave workgroup, pages staged in LDS): workgroup x runs
+// the page-range plan's workgroups 2 x and 2 x + 1.
+template <class C>
+__global__ __launch_bounds__(2 * C::NT) void decode_pair_kernel(BalArgs a) {
+    __shared__ PairShared<C> S;
+    pair_body<C>(a, S, blockIdx.x);
+}
+
 // The reference-shaped uniform split on the balanced body (items of equal key ranges, descriptors
 // built in the kernel from the device page table).
 template <class C>
@@ -1398,6 +1624,10 @@ using PartialCfg = Cfg<G, 16, 4, 2>;
 // flight only lengthen the memory queues.
 template <int G>
 using BalCfg = Cfg<G, 16, 4, 2>;
+// Paired decode: each kv head's half of the workgroup is two waves (the workgroup is still four
+// waves, one per SIMD), a two-page ring per wave in LDS.
+template <int G>
+using PairCfg = Cfg<G, 16, 2, 2>;
 
 template <class C>
 void launch_p(const PartialArgs& a, hipStream_t s) {
@@ -1407,6 +1637,10 @@ template <class C>
 void launch_b(const BalArgs& a, hipStream_t s) {
     if (a.ngroups > 0) decode_balanced_kernel<C, true><<<a.W, C::NT, 0, s>>>(a);
     else decode_balanced_kernel<C, false><<<a.W, C::NT, 0, s>>>(a);
+}
+template <class C>
+void launch_pair(const BalArgs& a, hipStream_t s) {
+    decode_pair_kernel<C><<<a.W / 2, 2 * C::NT, 0, s>>>(a);
 }
 template <class C>
 void launch_u(const UniArgs& a, hipStream_t s) {
@@ -1462,6 +1696,15 @@ hipError_t launch_merge_states(const float* part_o, const float* part_lse, _Floa
 hipError_t launch_decode_balanced(const BalArgs& a, int G, hipStream_t s) {
     if (G != 1 && G != 2 && G != 4 && G != 8) return hipErrorInvalidValue;
     PD_DISPATCH(BalCfg, G, launch_b, a, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_pair(const BalArgs& a, int G, hipStream_t s) {
+    if (G != 1 && G != 2 && G != 4) return hipErrorInvalidValue;
+    if (a.ngroups <= 0 || a.Hkv % 2 != 0 || a.W % 2 != 0 || a.W <= 0) return hipErrorInvalidValue;
+    if (G == 1) launch_pair<PairCfg<1>>(a, s);
+    else if (G == 2) launch_pair<PairCfg<2>>(a, s);
+    else launch_pair<PairCfg<4>>(a, s);
     return hipGetLastError();
 }
 

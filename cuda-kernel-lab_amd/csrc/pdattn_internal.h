@@ -184,6 +184,9 @@ hipError_t launch_decode_partial(const PartialArgs& a, int G, hipStream_t s);
 hipError_t launch_merge_states(const float* part_o, const float* part_lse, _Float16* out,
                                float* lse, int rows, int num_chunks, hipStream_t s);
 hipError_t launch_decode_balanced(const BalArgs& a, int G, hipStream_t s);
+// The paired variant of a page-range plan (two kv heads per workgroup, W / 2 workgroups; G in
+// 1, 2, 4 and Hkv even).
+hipError_t launch_decode_pair(const BalArgs& a, int G, hipStream_t s);
 hipError_t launch_decode_uniform(const UniArgs& a, int G, hipStream_t s);
 hipError_t launch_merge_split(const MergeArgs& a, int n_entries, hipStream_t s);
 hipError_t launch_decode_ranges(const DevArgs& a, int G, hipStream_t s);

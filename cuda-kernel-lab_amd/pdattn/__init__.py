@@ -94,7 +94,8 @@ class PlanInfo(ctypes.Structure):
                 ("split_pairs", ctypes.c_int), ("max_contributors", ctypes.c_int),
                 ("units", ctypes.c_int64), ("workspace_bytes", ctypes.c_size_t),
                 ("chunk_pages", ctypes.c_int), ("segments", ctypes.c_int),
-                ("merge_entries", ctypes.c_int), ("schedule_ints", ctypes.c_int)]
+                ("merge_entries", ctypes.c_int), ("schedule_ints", ctypes.c_int),
+                ("paired", ctypes.c_int)]
 
 
 class CascadeInfo(ctypes.Structure):

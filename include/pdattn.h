@@ -194,11 +194,18 @@ typedef struct pdattn_plan_info {
     int     segments;          /* segments over all workgroups                            */
     int     merge_entries;     /* pairs merged by the second launch (0: single launch)    */
     int     schedule_ints;     /* int32 count of pdattn_plan_get_schedule's output        */
+    int     paired;            /* 1: the decode launch runs workgroups w and w + 1 (kv heads
+                                  2k, 2k + 1 of one page range) as one workgroup of the paired
+                                  kernel, W / 2 workgroups                                 */
 } pdattn_plan_info;
 
 /* Build a plan from host copies of kv_indptr [B+1] and kv_last_page_len [B]. force_workgroups > 0
  * overrides the grid size (one workgroup per CU by default, two at G = 8; it grows when a
- * workgroup would exceed its segment or page limits). chunk_pages > 0, or a grid that is not a
+ * workgroup would exceed its segment or page limits). At G <= 4 with an even Hkv the default is
+ * first planned with two workgroups per CU for the paired kernel, which runs workgroups w and
+ * w + 1 (kv heads 2k, 2k + 1 of one page range) as one, its pages staged in LDS; if that plan
+ * splits any sequence over workgroups, one workgroup per CU is planned instead (info.paired).
+ * chunk_pages > 0, or a grid that is not a
  * multiple of Hkv, selects the other partition: chunks of up to chunk_pages pages (64 by default)
  * of one (sequence, kv head) pair, ordered sequence-major, then by chunk position, kv head
  * fastest, with workgroup w taking the page units [U w / W, U (w+1) / W) of that order (U = Hkv *
