@@ -336,7 +336,8 @@ def decode_workload(timer, lens, args, with_uniform, seed=11, nosplit=False):
     r = {"bytes": nbytes, "ms": ms, "steps": len(times[0]), "kernel_us": kern_us,
          "decode_kernel_us": dec_us, "merge_kernel_us": mrg_us,
          "kernel_launches": k, "kv_copies": ncopy, "workgroups": info.workgroups,
-         "split_pairs": info.split_pairs}
+         "split_pairs": info.split_pairs, "paired": info.paired,
+         "decode_kernel": "decode_pair_kernel" if info.paired else "decode_balanced_kernel"}
     if with_uniform:
         mu = statistics.median(times[1])
         r["uniform"] = {"us_per_step": round(mu * 1e3, 2), "chunks": nc,
@@ -364,6 +365,7 @@ def decode_leg(timer, lens, args, ceil, seed=11, reference=None):
     v, a = gbs(h["bytes"], h["ms"] * 1e-3), gbs(h["bytes"], h["kernel_us"] * 1e-6)
     out = {"B": len(lens), "L_mean": round(sum(lens) / len(lens), 1), "L_max": max(lens),
            "algorithmic_bytes": h["bytes"], "workgroups": h["workgroups"], "split_pairs": h["split_pairs"],
+           "decode_kernel": h["decode_kernel"],
            "us_per_step": round(h["ms"] * 1e3, 2), "GB/s": round(v, 1),
            "pct_of_peak": round(100 * v / PEAK_GBS, 1), "pct_of_ceiling": round(100 * v / ceil, 1),
            "kernel_us": round(h["kernel_us"], 2), "kernel_GB/s": round(a, 1),
@@ -651,6 +653,10 @@ TL_ROWS, TL_SLOTS = 8192, 32          # the stamp table of csrc/timeline.h
 DECODE_STAMPS = ([(0, "start"), (1, "descriptors staged"), (2, "q rows staged"), (3, "first ring step")]
                  + [(4 + 2 * s, f"segment {s} streamed") for s in range(12)]
                  + [(5 + 2 * s, f"segment {s} flushed") for s in range(12)] + [(31, "done")])
+# the paired kernel's stamp 2: its first page read back from LDS (q pieces go to registers)
+PAIR_STAMPS = ([(0, "start"), (1, "descriptors staged"), (2, "first page in registers"), (3, "first ring step")]
+                 + [(4 + 2 * s, f"segment {s} streamed") for s in range(12)]
+                 + [(5 + 2 * s, f"segment {s} flushed") for s in range(12)] + [(31, "done")])
 PREFIX_STAMPS = ([(0, "start"), (1, "ids staged"), (2, "block 0 in LDS")]
                  + [(3 + k, f"block {k} done") for k in range(24)]
                  + [(29, "blocks done"), (30, "partials written")])
@@ -711,7 +717,11 @@ def timeline(args):
         lens = [32768] if args.timeline == "32k" else [1024] * 64
         bt, t = make_device_batch(lens, 32, 8, seed=11)
         fn, plan, ws = plan_runner(bt, t, s)
-        W = plan.info().workgroups
+        info = plan.info()
+        W = info.workgroups // 2 if info.paired else info.workgroups   # workgroups of the launch
+        stamps = PAIR_STAMPS if info.paired else DECODE_STAMPS
+        print(json.dumps({"timeline": args.timeline, "kernel": "decode_pair_kernel" if info.paired
+                          else "decode_balanced_kernel", "launch_workgroups": W}), flush=True)
         reset("decode")
         runs = []
         for _ in range(reps):
@@ -720,7 +730,7 @@ def timeline(args):
             timer.flush()
             fn()
             runs.append(grab("decode"))
-        report(args.timeline, "cold", W, summary(runs, 0, W, DECODE_STAMPS))
+        report(args.timeline, "cold", W, summary(runs, 0, W, stamps))
         kv_bytes = 2 * t["k"].numel() * t["k"].element_size()
         n = max(2, -(-ROT_BYTES // kv_bytes))
         ks = [t["k"]] + [torch.empty_like(t["k"]).normal_() for _ in range(n - 1)]
@@ -731,7 +741,7 @@ def timeline(args):
                 plan.run(t["q"], ks[i % n], vs[i % n], t["indptr"], t["indices"], t["last"], t["out"],
                          t["lse"], ws, ws.numel(), stream=s)
             runs.append(grab("decode"))
-        report(args.timeline, "b2b", W, summary(runs, 0, W, DECODE_STAMPS))
+        report(args.timeline, "b2b", W, summary(runs, 0, W, stamps))
         return
     if args.timeline == "prefix":
         bt, t = make_device_batch(None, 32, 8, seed=21, shared_prefix=8192, suffix=[512] * 64)
@@ -847,7 +857,8 @@ def main():
         vs_baseline=None, dtype="f16", data="synthetic N(0,1) q/K/V, seeded, shuffled pages",
         config={"workload": name, "B": len(lens), "L": lens[0], "Hq": 32, "Hkv": 8,
                 "head_dim": 128, "page": 16, "seed": 11, "accumulate": "f32",
-                "path": "pdattn_plan_run (balanced decode launch + merge launch for split pairs)", "workgroups": h["workgroups"],
+                "path": f"pdattn_plan_run ({h['decode_kernel']} launch + merge launch for split pairs)",
+                "workgroups": h["workgroups"],
                 "algorithmic_bytes": h["bytes"], "cache_flush_bytes": FLUSH_BYTES,
                 "timing": "median of per-step HIP events, 1 GiB read flush before each step"},
         roofline={"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
@@ -855,9 +866,9 @@ def main():
                   "traffic_source": (f"{os.path.relpath(TRAFFIC_FILE, ROOT)}: rocprofv3 --pmc FETCH_SIZE / "
                                      f"WRITE_SIZE of the decode launch, copy-calibrated, collected at "
                                      f"commit {traffic_commit}" if traffic else None),
-                  "kernel": "one decode step = decode_balanced_kernel + merge_split_kernel (the merge "
+                  "kernel": f"one decode step = {h['decode_kernel']} + merge_split_kernel (the merge "
                             "launch runs when pairs are split); frac is the whole step's, both launches; "
-                            "kernel_frac is decode_balanced_kernel's alone (pdattn_plan_run_part, "
+                            f"kernel_frac is {h['decode_kernel']}'s alone (pdattn_plan_run_part, "
                             "decode launches back to back in this run)",
                   "kernel_us": round(h["kernel_us"], 2),
                   "kernel_frac": round(dec_achieved / PEAK_GBS, 4),
