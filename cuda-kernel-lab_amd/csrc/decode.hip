@@ -489,17 +489,24 @@ __device__ __forceinline__ void mstate_fold_dpp(MState& s) {
 
 __device__ __forceinline__ int merge_d0() { return 32 * (int)(threadIdx.x >> 6) + 4 * (int)((threadIdx.x & 63) >> 3); }
 
-// Loads sources k0 + r + 8 u (u < kMergeU) of list S (S.n > 0), unconditionally: a lane past the
-// last source reloads the last one, so every lane issues the same loads and no load waits for
-// another (conditional loads would make the compiler copy the results, and wait for them, where
-// the branches join).
-__device__ __forceinline__ void merge_load(const MSrc& S, int k0, float (&l)[kMergeU], float4 (&o)[kMergeU]) {
-    const int r = threadIdx.x & 7, d0 = merge_d0();
+// The sources of a row are list A then list B, as one list of A.n + B.n: source k is A's k-th
+// for k < A.n, else B's (k - A.n)-th. Lane r of each 8-lane group takes sources k0 + r + 8 u
+// (u < kMergeU), loaded unconditionally: a lane past the last source reloads the last one, and
+// the list a source comes from is a per-lane select of its address, so every lane issues the same
+// loads and no load waits for another (conditional loads would make the compiler copy the
+// results, and wait for them, where the branches join). 8 kMergeU sources per round trip.
+__device__ __forceinline__ void merge_load(const MSrc& A, const MSrc& B, int k0, float (&l)[kMergeU],
+                                           float4 (&o)[kMergeU]) {
+    const int r = threadIdx.x & 7, d0 = merge_d0(), n = A.n + B.n;
 #pragma unroll
     for (int u = 0; u < kMergeU; ++u) {
-        const size_t i = (size_t)min(k0 + r + 8 * u, S.n - 1) * S.stride;
-        l[u] = S.lse[i];
-        o[u] = *reinterpret_cast<const float4*>(S.o + i * kHeadDim + d0);
+        const int k = min(k0 + r + 8 * u, n - 1);
+        const bool inA = k < A.n;
+        const size_t i = inA ? (size_t)k * A.stride : (size_t)(k - A.n) * B.stride;
+        const float* lp = inA ? A.lse : B.lse;
+        const float* op = inA ? A.o : B.o;
+        l[u] = lp[i];
+        o[u] = *reinterpret_cast<const float4*>(op + i * kHeadDim + d0);
     }
 }
 // Folds this lane's loaded sources into s in order, branch-free (a dropped or empty source weighs 0
@@ -507,14 +514,16 @@ __device__ __forceinline__ void merge_load(const MSrc& S, int k0, float (&l)[kMe
 // loaded value used unconditionally, the compiler keeps all the loads ahead of the first wait.
 // For a kept source this is the online rule of lse_accumulate: the running state is rescaled by
 // exp(m - max(m, l)) (exactly 1 when l <= m) and the source added with weight exp(l - max(m, l)).
-template <class Keep>
-__device__ __forceinline__ void merge_fold(MState& s, const MSrc& S, int k0, const float (&l)[kMergeU],
-                                           const float4 (&o)[kMergeU], Keep keep) {
-    const int r = threadIdx.x & 7;
+// keepA(k) drops sources of list A (B's are all kept).
+template <class KeepA>
+__device__ __forceinline__ void merge_fold(MState& s, const MSrc& A, const MSrc& B, int k0,
+                                           const float (&l)[kMergeU], const float4 (&o)[kMergeU],
+                                           KeepA keepA) {
+    const int r = threadIdx.x & 7, n = A.n + B.n;
 #pragma unroll
     for (int u = 0; u < kMergeU; ++u) {
         const int k = k0 + r + 8 * u;
-        const bool ok = k < S.n && keep(k) && l[u] != -INFINITY;
+        const bool ok = k < n && (k >= A.n || keepA(k)) && l[u] != -INFINITY;
         const float lv = ok ? l[u] : -INFINITY;
         const float4 ov = ok ? o[u] : make_float4(0.f, 0.f, 0.f, 0.f);
         const float mn = fmaxf(s.m, lv);
@@ -531,26 +540,18 @@ __device__ __forceinline__ void merge_fold(MState& s, const MSrc& S, int k0, con
 
 template <class KeepA>
 __device__ __forceinline__ MState merge_lanes(const MSrc& A, const MSrc& B, KeepA keepA) {
-    constexpr int SPT = 8 * kMergeU;   // sources of a list per round trip
+    constexpr int SPT = 8 * kMergeU;   // sources per round trip
     MState s{-INFINITY, 0.f, make_float4(0.f, 0.f, 0.f, 0.f)};
-    float la[kMergeU], lb[kMergeU];
-    float4 oa[kMergeU], ob[kMergeU];
-    auto all = [](int) { return true; };
-    if (A.n > 0) merge_load(A, 0, la, oa);
-    if (B.n > 0) merge_load(B, 0, lb, ob);
-    __builtin_amdgcn_sched_barrier(0);   // every load above is issued before anything waits
-    if (A.n > 0) {
-        merge_fold(s, A, 0, la, oa, keepA);
-        for (int k0 = SPT; k0 < A.n; k0 += SPT) {
-            merge_load(A, k0, la, oa);
-            merge_fold(s, A, k0, la, oa, keepA);
-        }
-    }
-    if (B.n > 0) {
-        merge_fold(s, B, 0, lb, ob, all);
-        for (int k0 = SPT; k0 < B.n; k0 += SPT) {
-            merge_load(B, k0, lb, ob);
-            merge_fold(s, B, k0, lb, ob, all);
+    const int n = A.n + B.n;
+    if (n > 0) {
+        float l[kMergeU];
+        float4 o[kMergeU];
+        merge_load(A, B, 0, l, o);
+        __builtin_amdgcn_sched_barrier(0);   // every load above is issued before anything waits
+        merge_fold(s, A, B, 0, l, o, keepA);
+        for (int k0 = SPT; k0 < n; k0 += SPT) {
+            merge_load(A, B, k0, l, o);
+            merge_fold(s, A, B, k0, l, o, keepA);
         }
     }
     mstate_fold_dpp<0xB1>(s);    // quad_perm [1,0,3,2]
