@@ -378,8 +378,8 @@ def test_plan_workspace_written_by_the_caller(what):
 
 def test_all_empty_batch_with_an_empty_page_list():
     """Every sequence empty and kv_indices pointing just past the end of a buffer (no element):
-    the uniform split (one chunk and several), the plan path and decode_partial run without
-    reading it, and every row is 0 / -inf."""
+    the uniform split (one chunk and several), the device-range drop-in, the plan path and
+    decode_partial run without reading it, and every row is 0 / -inf."""
     import torch
     import pdattn
     print("[case] all-empty batch, kv_indices at the end of its buffer", flush=True)
@@ -408,6 +408,10 @@ def test_all_empty_batch_with_an_empty_page_list():
         try:
             pdattn.decode_attention(p, 4, out, lse, ws)
             check(f"decode_attention, {nc} chunks")
+            out.fill_(7.0)
+            lse.fill_(7.0)
+            pdattn.decode_attention_balanced(p, 4, out, lse, ws)
+            check(f"decode_attention_balanced, {nc} chunks")
         finally:
             pdattn.workspace_release(ws)
     plan = pdattn.Plan([0] * (B + 1), [0] * B, B, Hq, Hkv)
