@@ -124,6 +124,26 @@ def test_uniform_decode_attention_graph():
     pdattn.workspace_release(ws)
 
 
+def test_balanced_decode_attention_graph():
+    bt = inputs.make_batch([300, 5000, 17, 2048], 32, 8, seed=35)
+    db = DeviceBatch(bt)
+    print("graph: decode_attention_balanced", flush=True)
+    nc, ct = pdattn.plan_chunks(bt.G, bt.B, bt.Hkv, bt.max_len, 0)
+    p = db.params(nc, ct)
+    ws = pdattn.Workspace()
+    pdattn.workspace_reserve(ws, pdattn.decode_balanced_workspace_size(p, bt.G))
+    s = torch.cuda.current_stream()
+    pdattn.decode_attention_balanced(p, bt.G, db.out, db.lse, ws, s)
+    torch.cuda.synchronize()
+    _check_oracle(db, bt)
+    ref_o, ref_l = db.out.clone(), db.lse.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        pdattn.decode_attention_balanced(p, bt.G, db.out, db.lse, ws, torch.cuda.current_stream())
+    _replay_and_compare(g, db, ref_o, ref_l, "decode_attention_balanced")
+    pdattn.workspace_release(ws)
+
+
 def test_append_then_decode_graph():
     """A serving step as one graph: append each sequence's newest token, then decode."""
     lens = [700, 33, 1024]
