@@ -1,8 +1,8 @@
 """The timeline build of the library (make -C cuda-kernel-lab_amd timeline: the kernels compiled
 with per-workgroup timestamps, read by bench.py --timeline) computes exactly what the library
-proper computes, and its stamps come in phase order: the plan path's decode, the fused cascade
-step (decode and prefix roles, then the merge) and the prefix kernel alone with a partial last
-chunk, each compared bit for bit.
+proper computes, and its stamps come in phase order: the plan path's decode (one kv head per
+workgroup, and the paired kernel), the fused cascade step (decode and prefix roles, then the
+merge) and the prefix kernel alone with a partial last chunk, each compared bit for bit.
 
 The timeline build is loaded in a child process, so this process keeps the library proper.
 """
@@ -52,6 +52,26 @@ CHILD = textwrap.dedent(r"""
         seq = [row[0], row[1], row[2]] + [row[s] for s in range(4, 28) if row[s] > 0] + [row[31]]
         assert all(b >= a for a, b in zip(seq, seq[1:])), f"stamps out of order: {seq}"
     print("ok", int(ran.sum()), "workgroups stamped", flush=True)
+
+    # the paired kernel (a plan that splits no sequence: 64 x 1024 tokens on 256 CUs)
+    print("[case] paired kernel, timeline build vs library, 64 x 1024", flush=True)
+    bq = inputs.make_batch([1024] * 64, 32, 8, seed=52)
+    _, o0, l0, i0 = run(lib0, bq)
+    pdattn._lib = None
+    pdattn.LIB_PATH = sys.argv[2]
+    assert pdattn.lib().pdattn_timeline_reset_decode() == 0   # (no stamps left from the case above)
+    L, o1, l1, i1 = run(sys.argv[2], bq)
+    assert np.array_equal(o0, o1) and np.array_equal(l0, l1), "timeline build changed the paired results"
+    assert i0.paired == i1.paired
+    if i1.paired:
+        assert L.pdattn_timeline_read_decode(buf.ctypes.data, buf.nbytes) == 0
+        t = buf.reshape(8192, 32)[:i1.workgroups // 2].astype(np.int64)
+        ran = t[:, 0] > 0
+        assert ran.sum() > 0
+        for row in t[ran]:
+            seq = [row[0], row[1], row[2]] + [row[s] for s in range(4, 28) if row[s] > 0] + [row[31]]
+            assert all(b >= a for a, b in zip(seq, seq[1:])), f"paired stamps out of order: {seq}"
+        print("ok", int(ran.sum()), "paired workgroups stamped", flush=True)
 
     # the fused cascade step (decode role and prefix role in one launch, both stamped) and the
     # merge after it
