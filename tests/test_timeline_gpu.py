@@ -64,6 +64,8 @@ CHILD = textwrap.dedent(r"""
     assert np.array_equal(o0, o1) and np.array_equal(l0, l1), "timeline build changed the paired results"
     assert i0.paired == i1.paired
     if i1.paired:
+        # (a new handle: its functions need their argument types again, or the pointer is cut to an int)
+        L.pdattn_timeline_read_decode.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
         assert L.pdattn_timeline_read_decode(buf.ctypes.data, buf.nbytes) == 0
         t = buf.reshape(8192, 32)[:i1.workgroups // 2].astype(np.int64)
         ran = t[:, 0] > 0
