@@ -95,6 +95,42 @@ def test_prefix_kernel_partials(chunk_tokens, Lp):
     assert lens
 
 
+@pytest.mark.parametrize("B,Lp,chunk_tokens,scale", [(64, 1024, 256, 1.0), (70, 640, 96, 1.0), (33, 512, 64, -2.0)],
+                         ids=["64 seqs, two full groups", "70 seqs, 128 + 128 + 24 rows, partial last chunk",
+                              "33 seqs, 128 + 4 rows, negative scale"])
+def test_prefix_kernel_full_query_groups(B, Lp, chunk_tokens, scale):
+    """The prefix kernel with query groups that fill both tiles of every wave (128 rows of a kv head
+    per workgroup), ragged last groups (24 rows: two tiles in some waves only; 4 rows: one tile of
+    one wave), against the oracle's per-chunk partials."""
+    import torch
+    import _gpu
+    import pdattn
+    print(f"[case] prefix kernel B={B} Lp={Lp} chunk_tokens={chunk_tokens} scale={scale}", flush=True)
+    bt = inputs.make_shared_prefix_batch(Lp, [16] * B, 32, 8, seed=30 + B)
+    db = _gpu.DeviceBatch(bt)
+    nchunks = (Lp + chunk_tokens - 1) // chunk_tokens
+    rows = bt.B * bt.Hq
+    d = torch.device("cuda:0")
+    po = torch.full((rows, nchunks, 128), float("nan"), dtype=torch.float32, device=d)
+    pl = torch.full((rows, nchunks), float("nan"), dtype=torch.float32, device=d)
+    pp = pdattn.PrefixParams()
+    pp.q, pp.k_cache, pp.v_cache = db.q.data_ptr(), db.k.data_ptr(), db.v.data_ptr()
+    pp.prefix_pages = db.indices.data_ptr()
+    pp.part_o, pp.part_lse = po.data_ptr(), pl.data_ptr()
+    pp.B, pp.Hq, pp.Hkv = bt.B, bt.Hq, bt.Hkv
+    pp.prefix_len, pp.chunk_tokens, pp.part_stride = Lp, chunk_tokens, nchunks
+    pp.sm_scale = scale / np.sqrt(128)
+    pdattn.cascade_prefix(pp)
+    torch.cuda.synchronize()
+    indptr = np.arange(bt.B + 1, dtype=np.int32) * (Lp // 16)
+    indices = np.concatenate([bt.indices[bt.indptr[b]:bt.indptr[b] + Lp // 16] for b in range(bt.B)])
+    last = np.full(bt.B, 16, np.int32)
+    ro, rl = oracle.partials(bt.q, bt.k, bt.v, indptr, indices, last, bt.Hq, bt.Hkv, nchunks, chunk_tokens,
+                             sm_scale=scale / np.sqrt(128))
+    check_lse(pl.cpu().numpy(), rl, tag="prefix part_lse")
+    check_out(po.cpu().numpy(), ro, tag="prefix part_o")
+
+
 @pytest.mark.parametrize("B,chunk_tokens", [(1, 64), (2, 96), (4, 128), (5, 96), (8, 256)])
 def test_small_groups_are_deterministic(B, chunk_tokens):
     """Query groups of 4 to 32 rows (B x 4 heads here), which leave query tiles of the
