@@ -587,6 +587,7 @@ BalArgs bal_args(const pdattn_plan* pl, const void* q, const void* k, const void
     a.ngroups = pl->ngroups;
     a.nnz = pl->nnz;
     a.tag = pl->tag;
+    a.qrow_b = pl->ngroups > 0 && pl->B == 1 ? 0 : -1;
     return a;
 }
 

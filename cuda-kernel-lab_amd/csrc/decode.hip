@@ -831,7 +831,8 @@ struct BalShared {
 // wave streams its pages of all segments through one ring, flushing each segment at its end.
 // All threads of the workgroup call it.
 template <class C, bool COMPACT, bool RANGES>
-__device__ __forceinline__ void run_segments(const BalArgs& a, BalShared<C, COMPACT>& S, int nseg) {
+__device__ __forceinline__ void run_segments(const BalArgs& a, BalShared<C, COMPACT>& S, int nseg,
+                                             bool qpre = false) {
     constexpr int G = C::G, NW = C::NW, NT = C::NT, NBUF = C::NBUF, LPR = C::LPR;
     auto& sm = S.sm;
     int* pg = S.pg;
@@ -905,12 +906,14 @@ __device__ __forceinline__ void run_segments(const BalArgs& a, BalShared<C, COMP
         // (every load is issued, past the last segment from segment 0's rows, so that the number
         // of loads in flight is the same on every path and the waits below stay exact)
         u32x4 qv4[QMAX];
+        if (!qpre) {
 #pragma unroll
-        for (int k = 0; k < QMAX; ++k) {
-            const int j = tid + k * NT < nseg * QPS ? tid + k * NT : 0;
-            const int si = j / QPS;
-            const size_t row = (size_t)seg[si * kSegInts] * a.Hq + (size_t)seg[si * kSegInts + 1] * G;
-            qv4[k] = reinterpret_cast<const u32x4*>(qp + row * kHeadDim)[j % QPS];
+            for (int k = 0; k < QMAX; ++k) {
+                const int j = tid + k * NT < nseg * QPS ? tid + k * NT : 0;
+                const int si = j / QPS;
+                const size_t row = (size_t)seg[si * kSegInts] * a.Hq + (size_t)seg[si * kSegInts + 1] * G;
+                qv4[k] = reinterpret_cast<const u32x4*>(qp + row * kHeadDim)[j % QPS];
+            }
         }
         int pv[PMAX];
         if constexpr (!RANGES) {
@@ -928,9 +931,11 @@ __device__ __forceinline__ void run_segments(const BalArgs& a, BalShared<C, COMP
         // keeps the stores below after the loads above: the q rows are waited for while the
         // first pages are still in flight
         asm volatile("" ::: "memory");
+        if (!qpre) {
 #pragma unroll
-        for (int k = 0; k < QMAX; ++k)
-            if (tid + k * NT < nseg * QPS) qs[(tid + k * NT) / QPS][(tid + k * NT) % QPS] = qv4[k];
+            for (int k = 0; k < QMAX; ++k)
+                if (tid + k * NT < nseg * QPS) qs[(tid + k * NT) / QPS][(tid + k * NT) % QPS] = qv4[k];
+        }
         if constexpr (!RANGES) {
 #pragma unroll
             for (int k = 0; k < PMAX; ++k)
@@ -955,7 +960,7 @@ __device__ __forceinline__ void run_segments(const BalArgs& a, BalShared<C, COMP
         for (int h = 0; h < G; ++h)
 #pragma unroll
             for (int kk = 0; kk < C::PPL; ++kk) {
-                const u32x4 raw = qs[si][h * (kHeadDim / 8) + kk * LPR + c];
+                const u32x4 raw = qs[qpre ? 0 : si][h * (kHeadDim / 8) + kk * LPR + c];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) qv[h][kk][e] = as_h2(raw[e]);
             }
@@ -1229,10 +1234,12 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
     // known from the kernel arguments, so the page ids are loaded together with the descriptor
     // block, and the ring's first pages together with the q rows.
     int64_t lo = 0, hi = 0;
+    bool qpre = false;   // q rows staged in round trip 1 (a one-sequence page-range plan)
     if constexpr (RANGES) {
         const int64_t g = w / a.Hkv, nnz = kargs()->nnz, ng = kargs()->ngroups;
         lo = nnz * g / ng;
         hi = nnz * (g + 1) / ng;
+        qpre = kargs()->qrow_b >= 0;
     }
     int nseg;
     if constexpr (!UNI) {
@@ -1248,10 +1255,20 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
             const int i = tid + k * NT;
             pv[k] = i < npr ? kvi[i] : 0;
         }
+        // a one-sequence plan: the q rows of (qrow_b, this workgroup's kv head) in the same trip
+        // (every segment uses them), so that round trip 2 carries only the ring's first pages
+        u32x4 qv = {0u, 0u, 0u, 0u};
+        if constexpr (RANGES) {
+            if (qpre) {
+                const size_t row = (size_t)kargs()->qrow_b * a.Hq + (size_t)(w % a.Hkv) * G;
+                if (tid < QPS) qv = reinterpret_cast<const u32x4*>(kargs()->q + row * kHeadDim)[tid];
+            }
+        }
         if (tid < kBalDescInts) sd[tid] = dv;
 #pragma unroll
         for (int k = 0; k < PMAX; ++k)
             if (tid + k * NT < npr) pg[tid + k * NT] = pv[k];
+        if (qpre && tid < QPS) qs[0][tid] = qv;
         __syncthreads();
         PD_STAMP(1);
         nseg = __builtin_amdgcn_readfirstlane(sd[0]);
@@ -1297,7 +1314,7 @@ __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COM
         PD_STAMP(1);
     }
 
-    run_segments<C, COMPACT, RANGES>(a, S, nseg);
+    run_segments<C, COMPACT, RANGES>(a, S, nseg, qpre);
 }
 
 // ---- page ranges found on the device (the drop-in decode_attention without a host plan) -----

@@ -68,6 +68,9 @@ struct BalArgs {
     int ngroups;
     int nnz;
     int tag;                      // the plan's tag, expected in desc[1] of every block (host plans)
+    // >= 0 (page-range plans of one sequence): every segment of every workgroup is of sequence
+    // qrow_b, so a workgroup's q rows (kv head w % Hkv) are loaded with its descriptor block
+    int qrow_b = -1;
 };
 
 // The reference-shaped uniform split (decode_partial / decode_attention) run by the balanced
