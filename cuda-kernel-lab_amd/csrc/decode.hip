@@ -425,28 +425,6 @@ __device__ __forceinline__ KArgPtr kargs() {
 }
 
 // ---- merging partial states ----------------------------------------------------------------
-// Online log-sum-exp accumulation of one partial state (lse l, normalized output o) into
-// (m, ws, acc): acc / ws is the merged output, m + ln ws the merged lse. Empty states
-// (l = -inf) are identities.
-__device__ __forceinline__ void lse_accumulate(float& m, float& ws, float4& acc, float l, float4 o) {
-    if (l == -INFINITY) return;
-    if (l > m) {
-        const float sc = fast_exp2((m - l) * kLog2e);   // m = -inf gives 0
-        ws *= sc;
-        acc.x *= sc;
-        acc.y *= sc;
-        acc.z *= sc;
-        acc.w *= sc;
-        m = l;
-    }
-    const float w = fast_exp2((l - m) * kLog2e);
-    ws += w;
-    acc.x = fmaf(w, o.x, acc.x);
-    acc.y = fmaf(w, o.y, acc.y);
-    acc.z = fmaf(w, o.z, acc.z);
-    acc.w = fmaf(w, o.w, acc.w);
-}
-
 // Log-sum-exp merge of one row (128 dims) from partial states in a fixed order (merge_states,
 // 01_decode_attention.cu:238-255), by one workgroup of kMergeThreads = 4 waves, with no LDS and no
 // barrier. The sources are two lists, A then B (a pair's partial slots, then a cascade row's prefix
@@ -512,9 +490,10 @@ __device__ __forceinline__ void merge_load(const MSrc& A, const MSrc& B, int k0,
 // Folds this lane's loaded sources into s in order, branch-free (a dropped or empty source weighs 0
 // and its values are replaced, not multiplied, so unused slots may hold anything): with every
 // loaded value used unconditionally, the compiler keeps all the loads ahead of the first wait.
-// For a kept source this is the online rule of lse_accumulate: the running state is rescaled by
-// exp(m - max(m, l)) (exactly 1 when l <= m) and the source added with weight exp(l - max(m, l)).
-// keepA(k) drops sources of list A (B's are all kept).
+// For a kept source this is the online log-sum-exp rule: the running state (m, ws, acc) is rescaled
+// by exp(m - max(m, l)) (exactly 1 when l <= m) and the source (lse l, normalized output o) added
+// with weight exp(l - max(m, l)); an empty source (l = -inf) weighs 0. keepA(k) drops sources of
+// list A (B's are all kept).
 template <class KeepA>
 __device__ __forceinline__ void merge_fold(MState& s, const MSrc& A, const MSrc& B, int k0,
                                            const float (&l)[kMergeU], const float4 (&o)[kMergeU],
@@ -1207,28 +1186,21 @@ template <class C, bool UNI = false, bool COMPACT = false, bool RANGES = false>
 __device__ __forceinline__ void balanced_body(const BalArgs& a, BalShared<C, COMPACT>& S, int w,
                                               const UniArgs* u = nullptr) {
     static_assert(!(UNI && RANGES), "the uniform split builds its own descriptors");
-    constexpr int G = C::G, NW = C::NW, NT = C::NT, NBUF = C::NBUF, LPR = C::LPR;
-    auto& sm = S.sm;
+    constexpr int G = C::G, NT = C::NT;
     int* pg = S.pg;
     auto& qs = S.qs;
     int* sd = S.sd;
-    // the wave index is made wave-uniform explicitly: everything the page ring derives from it
-    // (per-wave page counts, page ids, buffer resources) must live in scalar registers
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int r = lane / LPR, c = lane % LPR;
-    // Segment fields are staged in LDS and read back wave-uniform: global (vector) loads of them
-    // would count against the same wait counter as the ring's page loads, and a non-uniform value
-    // in a buffer resource would turn every page load into a loop over lanes. sd holds the
-    // descriptor block: a header of 8 ints, then the segments.
+    const int tid = threadIdx.x;
+    // Segment fields are staged in LDS (sd: a header of 8 ints, then the segments) and read back
+    // wave-uniform by run_segments: global (vector) loads of them would count against the same
+    // wait counter as the ring's page loads, and a non-uniform value in a buffer resource would
+    // turn every page load into a loop over lanes.
     int* seg = sd + 8;
-    auto fld = [&](int si, int f) { return __builtin_amdgcn_readfirstlane(seg[si * kSegInts + f]); };
     // timestamps (timeline build only): 0 start, 1 descriptors (and page ids) staged, 2 q rows
     // staged, 3 the first ring step computed, 4 + 2 s / 5 + 2 s segment s streamed / flushed
     // (s < 12), 31 done; thread 0 of the workgroup
     PD_STAMP(0);
     constexpr int PMAX = kRangeMax / NT, QPS = G * kHeadDim / 8;
-    constexpr int QMAX = (BalShared<C, COMPACT>::SEGS * QPS + NT - 1) / NT;
     // A page-range plan (RANGES: ngroups > 0) gives workgroup w = g * Hkv + kvh the pages
     // [lo, hi) of the page table (relative to kv_indptr[0]), lo = nnz g / ngroups: its page list is
     // known from the kernel arguments, so the page ids are loaded together with the descriptor
