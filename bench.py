@@ -240,11 +240,25 @@ def rotated_kernel_us(plan, ws, t, stream, steps, parts=None):
     return e0.elapsed_time(e1) * 1e3 / k, k, n
 
 
+def kernel_sources_sha():
+    """sha256 (first 16 hex digits) of the library's sources: every file of
+    cuda-kernel-lab_amd/csrc and include/pdattn.h, in name order. The profile summaries record the
+    same digest, so a figure read from them can be matched to the kernels this run measures."""
+    import hashlib
+    h = hashlib.sha256()
+    csrc = os.path.join(ROOT, "cuda-kernel-lab_amd", "csrc")
+    files = [os.path.join(csrc, n) for n in sorted(os.listdir(csrc))] + [os.path.join(ROOT, "include", "pdattn.h")]
+    for path in files:
+        with open(path, "rb") as f:
+            h.update(os.path.basename(path).encode() + b"\0" + f.read())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic():
-    """(HBM bytes per launch of the headline kernel, commit the counters were collected on) from the
-    committed counter summary (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by its copy-kernel
-    calibration), or (None, None)."""
-    nbytes, commit = None, None
+    """(HBM bytes per launch of the headline kernel, commit and kernel-source digest the counters
+    were collected on) from the committed counter summary (FETCH_SIZE + WRITE_SIZE per dispatch,
+    each scaled by its copy-kernel calibration), or Nones."""
+    nbytes, commit, sha = None, None, None
     try:
         with open(TRAFFIC_FILE) as f:
             for line in f:
@@ -252,9 +266,11 @@ def measured_traffic():
                     nbytes = int(float(line.split(":", 1)[1]))
                 elif line.startswith("commit:"):
                     commit = line.split(":", 1)[1].strip()
+                elif line.startswith("kernel_sources_sha256:"):
+                    sha = line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return nbytes, commit
+    return nbytes, commit, sha
 
 
 def copy_calibration(steps):
@@ -848,7 +864,9 @@ def main():
                         nosplit=args.only in ("", "32k", "64x1k"))
     value = gbs(h["bytes"], h["ms"] * 1e-3)
     achieved = gbs(h["bytes"], h["kernel_us"] * 1e-6)
-    traffic, traffic_commit = measured_traffic() if not args.only or args.only == "32k" else (None, None)
+    traffic, traffic_commit, traffic_sha = (measured_traffic() if not args.only or args.only == "32k"
+                                            else (None, None, None))
+    sources_sha = kernel_sources_sha()
     dec_achieved = gbs(h["bytes"], h["decode_kernel_us"] * 1e-6)
     result = dict(
         metric=METRIC, value=round(value, 1), unit="GB/s", n_gpus=1, steps=h["steps"],
@@ -866,6 +884,7 @@ def main():
                   "traffic_source": (f"{os.path.relpath(TRAFFIC_FILE, ROOT)}: rocprofv3 --pmc FETCH_SIZE / "
                                      f"WRITE_SIZE of the decode launch, copy-calibrated, collected at "
                                      f"commit {traffic_commit}" if traffic else None),
+                  "traffic_sources_match": (traffic_sha == sources_sha) if traffic else None,
                   "kernel": f"{h['decode_kernel']}, the dominant kernel: achieved = the algorithmic bytes "
                             "of one launch / its average duration, decode launches alone "
                             "(pdattn_plan_run_part) back to back over rotated K/V copies between one "
@@ -882,6 +901,7 @@ def main():
                   "timing": f"{h['kernel_launches']} back-to-back launches over {h['kv_copies']} "
                             f"K/V copies (>= 1 GiB) between one event pair"},
         device={"arch": dinfo.arch.decode(), "cus": dinfo.compute_units},
+        kernel_sources_sha256=sources_sha,
     )
     if "uniform" in h:
         result["uniform_path"] = h["uniform"]
