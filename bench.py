@@ -489,15 +489,16 @@ def cascade_workload(timer, args, Hq=32, Hkv=8):
 
 def prefix_workload(timer, args):
     """The cascade's MFMA prefix pass alone (pdattn_cascade_prefix) on the benchmark's shared
-    prefix: 64 requests x 8192 shared tokens, chunks of 256 tokens (32 chunks x 2 query groups
-    of 128 rows x 8 kv heads = 512 workgroups). Flops per launch: 4 x (B Hq rows) x 128 x 8192
-    (QK^T and PV, 2 each)."""
+    prefix: 64 requests x 8192 shared tokens, chunks of 512 tokens. With 256 query rows per kv head
+    the pass runs the key-split kernel: 16 chunks x 2 query groups of 128 rows x 8 kv heads = 256
+    workgroups, one per CU, each splitting its chunk's keys between two wave groups. Flops per
+    launch: 4 x (B Hq rows) x 128 x 8192 (QK^T and PV, 2 each)."""
     import numpy as np
     import torch
     import pdattn
     s = timer.stream
     d = torch.device("cuda:0")
-    Lp, ct = 8192, 256
+    Lp, ct = 8192, 512
     bt, t = make_device_batch(None, 32, 8, seed=21, shared_prefix=Lp, suffix=[512] * 64)
     nch = Lp // ct
     rows = bt.B * 32
@@ -525,7 +526,8 @@ def prefix_workload(timer, args):
     flops = 4.0 * rows * 128 * Lp
     del t, po, pl
     qgroups = -(-(bt.B * 32 // 8) // 128)   # 128 stacked query rows per workgroup, per kv head
-    return {"flops": flops, "workgroups": nch * qgroups * 8, "cold_us": round(cold * 1e6, 2),
+    return {"flops": flops, "chunk_tokens": ct, "workgroups": nch * qgroups * 8,
+            "partial_bytes": rows * nch * (128 + 1) * 4, "cold_us": round(cold * 1e6, 2),
             "cold_TFLOP/s": round(flops / cold / 1e12, 1),
             "back_to_back_us": round(hot * 1e6, 2), "TFLOP/s": round(flops / hot / 1e12, 1),
             "frac_of_fp16_mfma_peak": round(flops / hot / 2.5e15, 4), "peak_TFLOP/s": 2500.0}

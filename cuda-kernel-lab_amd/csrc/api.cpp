@@ -1337,9 +1337,7 @@ int pdattn_cascade_prefix(const pdattn_prefix_params* p, void* stream) {
     const size_t slots = (size_t)p->B * p->Hq * p->part_stride;
     res_written(p->part_o, slots * kHeadDim * sizeof(float));
     res_written(p->part_lse, slots * sizeof(float));
-    const int rows = prefix_rows_per_workgroup();
-    const int qtiles = (p->B * G + rows - 1) / rows;
-    PD_HIP(launch_cascade_prefix(a, G, qtiles, static_cast<hipStream_t>(stream)));
+    PD_HIP(launch_cascade_prefix(a, G, static_cast<hipStream_t>(stream)));
     return PDATTN_OK;
 }
 
@@ -1462,7 +1460,7 @@ int pdattn_cascade_decode(pdattn_cascade_plan* cp, void* out, float* lse, pdattn
         PD_HIP(hipStreamWaitEvent(cp->aux, cp->ev_fork, 0));
         ps = cp->aux;
     }
-    PD_HIP(launch_cascade_prefix(a, p.Hq / p.Hkv, 1, ps));
+    PD_HIP(launch_cascade_prefix(a, p.Hq / p.Hkv, ps));
     if (two) PD_HIP(hipEventRecord(cp->ev_join, ps));
     return run_plan(&cp->sk, p.q, p.k_cache, p.v_cache, sind, sidx, p.kv_last_page_len, p.sm_scale,
                     out, lse, skb, cp->sk.ws_bytes, s, ppo, pplse, cp->n_extra,

@@ -195,7 +195,7 @@ hipError_t launch_merge_split(const MergeArgs& a, int n_entries, hipStream_t s);
 hipError_t launch_decode_ranges(const DevArgs& a, int G, hipStream_t s);
 hipError_t launch_merge_ranges(const DevMergeArgs& a, hipStream_t s);
 hipError_t launch_fill_i32(int32_t* p, int32_t value, size_t n, hipStream_t s);
-hipError_t launch_cascade_prefix(const PrefixArgs& a, int G, int qtiles, hipStream_t s);
+hipError_t launch_cascade_prefix(const PrefixArgs& a, int G, hipStream_t s);
 hipError_t launch_cascade_step(const StepArgs& a, int G, hipStream_t s);
 hipError_t launch_append_kv(const AppendArgs& a, int cus, hipStream_t s);
 hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, int grid, hipStream_t s);

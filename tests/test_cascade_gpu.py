@@ -95,13 +95,20 @@ def test_prefix_kernel_partials(chunk_tokens, Lp):
     assert lens
 
 
-@pytest.mark.parametrize("B,Lp,chunk_tokens,scale", [(64, 1024, 256, 1.0), (70, 640, 96, 1.0), (33, 512, 64, -2.0)],
-                         ids=["64 seqs, two full groups", "70 seqs, 128 + 128 + 24 rows, partial last chunk",
-                              "33 seqs, 128 + 4 rows, negative scale"])
+@pytest.mark.parametrize("B,Lp,chunk_tokens,scale",
+                         [(64, 1024, 256, 1.0), (70, 640, 96, 1.0), (33, 512, 64, -2.0), (64, 8240, 8192, 1.0),
+                          (48, 992, 160, 0.5), (32, 704, 128, 1.0), (40, 64, 64, 1.0)],
+                         ids=["64 seqs, two full 128-row groups", "70 seqs, 128 + 128 + 24 rows, partial last chunk",
+                              "33 seqs, 128 + 4 rows, negative scale", "64 seqs, 8192-token chunk + 48-token chunk",
+                              "48 seqs, 128 + 64 rows, 3-block chunks with a partial block",
+                              "32 seqs, 128 rows (the 4-wave body)", "40 seqs, one block per chunk"])
 def test_prefix_kernel_full_query_groups(B, Lp, chunk_tokens, scale):
-    """The prefix kernel with query groups that fill both tiles of every wave (128 rows of a kv head
-    per workgroup), ragged last groups (24 rows: two tiles in some waves only; 4 rows: one tile of
-    one wave), against the oracle's per-chunk partials."""
+    """The prefix kernel with more than 128 query rows per kv head, which runs the 8-wave key-split
+    body (128 rows per workgroup, the chunk's blocks split between two wave groups and combined in
+    LDS): full groups (both tiles of every wave), ragged groups (24 and 4 rows: one tile of some
+    waves; 64 rows: one tile of every wave), chunks of one block (the second wave group idle), two,
+    three (the last partial, on the second group) and 128 blocks, and the 4-wave body at exactly
+    128 rows; against the oracle's per-chunk partials."""
     import torch
     import _gpu
     import pdattn
