@@ -24,21 +24,19 @@ __global__ __launch_bounds__(kPrefixThreads, 2) void cascade_prefix_kernel(Prefi
 //
 // Waves 0-3 (group 0) take the chunk's first ceil(nblk / 2) 64-key blocks and waves 4-7 (group 1)
 // the rest; wave w and wave w + 4 hold the same 32 query rows, and each SIMD holds one wave of each
-// group. A wave alternates an MFMA phase (the PV product of block m - 1, then the scores of block
-// m) with a VALU phase (the online softmax of block m, then its share of the group's staging).
-// Group 1 runs one phase behind group 0 and a workgroup barrier ends every phase, so on each SIMD
-// one wave's MFMAs execute while the other's VALU work issues: the matrix core and the VALU are
-// busy at once, which waves that reach the same phase together do not arrange. At the end wave
+// group. A step of a wave is an MFMA phase (the PV product of block i - 1, then the scores of block
+// i) and a VALU phase (the online softmax of a block); group 0 runs them in that order, group 1 the
+// other way round (the softmax of block i - 1 first), so each step starts with one wave's MFMAs
+// beside the other's VALU work on every SIMD. One workgroup barrier per step. At the end wave
 // w + 4 hands its (maximum, sum, accumulators) to wave w through LDS, and wave w writes the
 // chunk's partial: one partial per row for the 2 x 256 keys of a 512-token chunk, half the partial
 // bytes that 256-row workgroups over 256-token chunks write for the same work per workgroup.
 //
 // Each group stages its own blocks, K and V, into two LDS buffers each, by direct global->LDS
-// loads (global_load_lds_dwordx4: no registers, no LDS store instructions). Block j's K is read by
-// the scores in MFMA phase j and its V by the PV product in MFMA phase j + 1, so in VALU phase m a
-// wave issues K of block m + 2 (its buffer's last reader, the scores of block m, is done) and V of
-// block m + 1 (the PV product of block m - 1 is done), and waits for the loads it issued in the
-// previous VALU phase (K of block m + 1, V of block m): two phases between issue and use.
+// loads (global_load_lds_dwordx4: no registers, no LDS store instructions). Block i's K is read
+// by the scores in step i and its V by the PV product in step i + 1, so after the barrier that
+// starts step i a wave issues K of block i + 1 and V of block i (their buffers' last readers ran
+// in step i - 1) and waits for them at the end of the step.
 constexpr int kKSWaves = 8;
 constexpr int kKSThreads = kKSWaves * 64;
 constexpr int kKSRows = 4 * kPrefixTiles * 16;   // 128 query rows per workgroup
@@ -201,12 +199,9 @@ __device__ __forceinline__ void prefix_chunk_ks(const PrefixArgs& a, KSSmem& sm,
         for (int dt = 0; dt < 8; ++dt) acc[tq][dt] = pf32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    // K of block 0 (group 0: landed with the q rows), V of block 0 and K of block 1 on their way;
-    // group 1 waits for its K of block 0 in its first (otherwise idle) phase
+    // K of block 0 in LDS before the first step (group 0's full first block landed with the q rows)
     if (nbg > 0 && !k0) dma(0, false);
-    if (nbg > 0) dma(0, true);
-    if (nbg > 1) dma(1, false);
-    if (grp == 0 && !k0) ks_wait_loads(nbg > 1 ? 8 : 4);
+    ks_wait_loads(0);
     ks_barrier();
     PD_STAMP(2);
 
@@ -341,50 +336,40 @@ __device__ __forceinline__ void prefix_chunk_ks(const PrefixArgs& a, KSSmem& sm,
         else
             softmax(m, std::true_type{});
     };
-    // the rest of VALU phase m: K of block m + 2 and V of block m + 1 on their way, then the loads
-    // of the previous VALU phase (K of block m + 1, V of block m) landed
-    auto stage = [&](int m) {
-        int n = 0;
-        if (m + 2 < nbg) {
-            dma(m + 2, false);
-            n += 4;
-        }
-        if (m + 1 < nbg) {
-            dma(m + 1, true);
-            n += 4;
-        }
-        ks_wait_loads(n);
+    // Block loads of step i, issued after the barrier that starts it: K of block i + 1 (its buffer's
+    // last reader, the scores of block i - 1, ran in step i - 1) and V of block i (the PV product of
+    // block i - 2 ran in step i - 1); waited for at the end of the step, before the barrier that
+    // starts step i + 1, where they are read.
+    auto issue = [&](int i) {
+        if (i + 1 < nbg) dma(i + 1, false);
+        if (i < nbg) dma(i, true);
     };
 
-    // The phases, one loop per group (each straight-line, so the register allocator sees no merge
-    // of the two groups' phase orders); both loops pass the same 2 nsteps + 1 barriers. Group 0,
-    // step i: MFMA phase i (pv(i - 1), qk(i)), then VALU phase i. Group 1, one phase behind: VALU
-    // phase i - 1, then MFMA phase i.
+    // The steps, one loop per group (each straight-line), one barrier per step. Group 0, step i:
+    // MFMA phase (pv(i - 1), qk(i)), then VALU phase (softmax of block i). Group 1: VALU phase
+    // (softmax of block i - 1), then MFMA phase (pv(i - 1), qk(i)). On each SIMD one wave of each
+    // group, so a step starts with one wave's MFMAs beside the other's VALU work, and from there
+    // the two waves overlap as their phases allow.
     if (grp == 0) {
         for (int i = 0; i <= nsteps; ++i) {
+            issue(i);
             if (i >= 1) pv(i - 1);
             if (i < nbg) qk(i);
             if (i >= 1 && i - 1 < 24) PD_STAMP(3 + i - 1);
+            if (i < nsteps) valu_phase(i);
+            ks_wait_loads(0);
             ks_barrier();
-            if (i < nsteps) {
-                valu_phase(i);
-                stage(i);
-                ks_barrier();
-            }
         }
     } else {
         for (int i = 0; i <= nsteps; ++i) {
-            if (i >= 1 && i - 1 < nbg) valu_phase(i - 1);
-            if (i >= 1)
-                stage(i - 1);
-            else if (nbg > 0)
-                ks_wait_loads(nbg > 1 ? 8 : 4);   // K of block 0
-            ks_barrier();
-            if (i >= 1 && i - 1 < nbg) pv(i - 1);
-            if (i < nsteps) {
-                if (i < nbg) qk(i);
-                ks_barrier();
+            issue(i);
+            if (i >= 1 && i - 1 < nbg) {
+                valu_phase(i - 1);
+                pv(i - 1);
             }
+            if (i < nbg) qk(i);
+            ks_wait_loads(0);
+            ks_barrier();
         }
     }
     PD_STAMP(29);

@@ -2,7 +2,8 @@
 with per-workgroup timestamps, read by bench.py --timeline) computes exactly what the library
 proper computes, and its stamps come in phase order: the plan path's decode (one kv head per
 workgroup, and the paired kernel), the fused cascade step (decode and prefix roles, then the
-merge) and the prefix kernel alone with a partial last chunk, each compared bit for bit.
+merge) and the prefix kernel alone with a partial last chunk (its 4-wave and key-split bodies),
+each compared bit for bit.
 
 The timeline build is loaded in a child process, so this process keeps the library proper.
 """
@@ -90,43 +91,48 @@ CHILD = textwrap.dedent(r"""
     assert np.array_equal(res[0][0], res[1][0]) and np.array_equal(res[0][1], res[1][1]), \
         "timeline build changed the fused cascade step's results"
 
-    # the prefix kernel alone, with a partial last chunk (640 keys in chunks of 96: 6 full + 64)
-    print("[case] prefix kernel, timeline build vs library, 640 keys in chunks of 96", flush=True)
-    bp = inputs.make_shared_prefix_batch(640, [3, 20, 50], 32, 8, seed=8)
-    nch, rows = 7, bp.B * bp.Hq
-    res = []
-    for path in (lib0, sys.argv[2]):
-        pdattn._lib = None
-        pdattn.LIB_PATH = path
-        Lp = pdattn.lib()
-        if path != lib0:
-            assert Lp.pdattn_timeline_reset_prefix() == 0
-        db = _gpu.DeviceBatch(bp)
-        po = torch.full((rows, nch, 128), float("nan"), dtype=torch.float32, device="cuda:0")
-        pl = torch.full((rows, nch), float("nan"), dtype=torch.float32, device="cuda:0")
-        pp = pdattn.PrefixParams()
-        pp.q, pp.k_cache, pp.v_cache = db.q.data_ptr(), db.k.data_ptr(), db.v.data_ptr()
-        pp.prefix_pages = db.indices.data_ptr()
-        pp.part_o, pp.part_lse = po.data_ptr(), pl.data_ptr()
-        pp.B, pp.Hq, pp.Hkv = bp.B, bp.Hq, bp.Hkv
-        pp.prefix_len, pp.chunk_tokens, pp.part_stride = 640, 96, nch
-        pp.sm_scale = 1.0 / np.sqrt(128)
-        pdattn.cascade_prefix(pp)
-        torch.cuda.synchronize()
-        res.append((po.cpu().numpy(), pl.cpu().numpy()))
-    assert np.array_equal(res[0][0].view(np.int32), res[1][0].view(np.int32)) and \
-        np.array_equal(res[0][1].view(np.int32), res[1][1].view(np.int32)), \
-        "timeline build changed the prefix kernel's partials"
-    Lp.pdattn_timeline_read_prefix.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
-    buf = np.zeros(8192 * 32, np.uint64)
-    assert Lp.pdattn_timeline_read_prefix(buf.ctypes.data, buf.nbytes) == 0
-    nwg = nch * 1 * bp.Hkv          # grid (chunks, query groups = 1, kv heads)
-    t = buf.reshape(8192, 32)[:nwg].astype(np.int64)
-    assert (t[:, 0] > 0).all(), "a prefix workgroup left no stamps"
-    for row in t:
-        seq = [row[0], row[1], row[2]] + [row[s] for s in range(3, 27) if row[s] > 0] + [row[29], row[30]]
-        assert all(b >= a for a, b in zip(seq, seq[1:])), f"prefix stamps out of order: {seq}"
-    print("ok prefix", nwg, "workgroups stamped", flush=True)
+    # the prefix kernel alone, with a partial last chunk: 12 rows per kv head (the 4-wave body;
+    # 640 keys in chunks of 96: 6 full + 64), and 192 rows (the key-split body, two query groups;
+    # 992 keys in chunks of 160: 6 full + 32, three blocks split 2 + 1 between the wave groups)
+    for Lpre, seqs, ct, nch, qg, tag in ((640, [3, 20, 50], 96, 7, 1, "4-wave"),
+                                        (992, [16] * 48, 160, 7, 2, "key-split")):
+        print(f"[case] prefix kernel ({tag}), timeline build vs library, {Lpre} keys in chunks of {ct}",
+              flush=True)
+        bp = inputs.make_shared_prefix_batch(Lpre, seqs, 32, 8, seed=8)
+        rows = bp.B * bp.Hq
+        res = []
+        for path in (lib0, sys.argv[2]):
+            pdattn._lib = None
+            pdattn.LIB_PATH = path
+            Lp = pdattn.lib()
+            if path != lib0:
+                assert Lp.pdattn_timeline_reset_prefix() == 0
+            db = _gpu.DeviceBatch(bp)
+            po = torch.full((rows, nch, 128), float("nan"), dtype=torch.float32, device="cuda:0")
+            pl = torch.full((rows, nch), float("nan"), dtype=torch.float32, device="cuda:0")
+            pp = pdattn.PrefixParams()
+            pp.q, pp.k_cache, pp.v_cache = db.q.data_ptr(), db.k.data_ptr(), db.v.data_ptr()
+            pp.prefix_pages = db.indices.data_ptr()
+            pp.part_o, pp.part_lse = po.data_ptr(), pl.data_ptr()
+            pp.B, pp.Hq, pp.Hkv = bp.B, bp.Hq, bp.Hkv
+            pp.prefix_len, pp.chunk_tokens, pp.part_stride = Lpre, ct, nch
+            pp.sm_scale = 1.0 / np.sqrt(128)
+            pdattn.cascade_prefix(pp)
+            torch.cuda.synchronize()
+            res.append((po.cpu().numpy(), pl.cpu().numpy()))
+        assert np.array_equal(res[0][0].view(np.int32), res[1][0].view(np.int32)) and \
+            np.array_equal(res[0][1].view(np.int32), res[1][1].view(np.int32)), \
+            f"timeline build changed the prefix kernel's partials ({tag})"
+        Lp.pdattn_timeline_read_prefix.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+        buf = np.zeros(8192 * 32, np.uint64)
+        assert Lp.pdattn_timeline_read_prefix(buf.ctypes.data, buf.nbytes) == 0
+        nwg = nch * qg * bp.Hkv          # grid (chunks, query groups, kv heads)
+        t = buf.reshape(8192, 32)[:nwg].astype(np.int64)
+        assert (t[:, 0] > 0).all(), f"a prefix workgroup left no stamps ({tag})"
+        for row in t:
+            seq = [row[0], row[1], row[2]] + [row[s] for s in range(3, 27) if row[s] > 0] + [row[29], row[30]]
+            assert all(b >= a for a, b in zip(seq, seq[1:])), f"prefix stamps out of order ({tag}): {seq}"
+        print("ok prefix", tag, nwg, "workgroups stamped", flush=True)
 """)
 
 
@@ -135,4 +141,4 @@ def test_timeline_build_matches_library_and_stamps_in_order():
     r = subprocess.run([sys.executable, "-c", CHILD, ROOT, TL_LIB], capture_output=True, text=True,
                        timeout=110)
     assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-2000:]
-    assert "ok prefix" in r.stdout
+    assert "ok prefix 4-wave" in r.stdout and "ok prefix key-split" in r.stdout
