@@ -425,15 +425,18 @@ __device__ __forceinline__ void prefix_chunk_ks(const PrefixArgs& a, KSSmem& sm,
 }
 
 // One workgroup per CU: 8 waves of at most 256 VGPRs fill each SIMD's registers, and the four
-// key buffers take 134 KB of LDS.
+// key buffers take 134 KB of LDS. Workgroup (x, y) = (query group * Hkv + kv head, chunk):
+// workgroups go to the XCDs round robin, so with Hkv a multiple of 8 every chunk of a (query group,
+// kv head) runs on one XCD, whose L2 then holds whole stretches of each row's partials (a row's
+// chunks are adjacent in memory) when they are written back.
 __global__ __launch_bounds__(kKSThreads, 1) void cascade_prefix_ks_kernel(PrefixArgs a) {
     __shared__ KSSmem sm;
-    const int qgrp = blockIdx.y;
+    const int qgrp = blockIdx.x / a.Hkv, kvh = blockIdx.x % a.Hkv;
     const int rows = a.ns * (a.Hq / a.Hkv) - qgrp * kKSRows;
     if (rows > 16 * 4)
-        prefix_chunk_ks<kPrefixTiles>(a, sm, blockIdx.x, qgrp, blockIdx.z);
+        prefix_chunk_ks<kPrefixTiles>(a, sm, blockIdx.y, qgrp, kvh);
     else
-        prefix_chunk_ks<1>(a, sm, blockIdx.x, qgrp, blockIdx.z);
+        prefix_chunk_ks<1>(a, sm, blockIdx.y, qgrp, kvh);
 }
 
 }  // namespace
@@ -451,7 +454,7 @@ hipError_t launch_cascade_prefix(const PrefixArgs& a, int G, hipStream_t s) {
     const int rows = a.ns * G;
     if (a.num_chunks <= 0 || rows <= 0) return hipSuccess;
     if (rows > kPrefixRows && !a.seqs) {
-        dim3 grid(a.num_chunks, (rows + kKSRows - 1) / kKSRows, a.Hkv);
+        dim3 grid((rows + kKSRows - 1) / kKSRows * a.Hkv, a.num_chunks);
         cascade_prefix_ks_kernel<<<grid, kKSThreads, 0, s>>>(a);
         return hipGetLastError();
     }
