@@ -109,11 +109,26 @@ def test_prefix_kernel_full_query_groups(B, Lp, chunk_tokens, scale):
     waves; 64 rows: one tile of every wave), chunks of one block (the second wave group idle), two,
     three (the last partial, on the second group) and 128 blocks, and the 4-wave body at exactly
     128 rows; against the oracle's per-chunk partials."""
+    _prefix_partials_vs_oracle(B, Lp, chunk_tokens, scale, 32, 8)
+
+
+@pytest.mark.parametrize("Hq,Hkv,B,Lp,chunk_tokens",
+                         [(64, 8, 20, 640, 128), (8, 2, 40, 512, 64), (64, 16, 40, 256, 16), (128, 16, 36, 320, 96)],
+                         ids=["G8 160 rows", "Hkv2 G4 160 rows", "Hkv16 16-token chunks", "Hkv16 G8 288 rows"])
+def test_prefix_key_split_head_layouts(Hq, Hkv, B, Lp, chunk_tokens):
+    """The key-split body at other head layouts: G = 8; Hkv = 2, whose grid width (query groups x
+    kv heads = 4) is not a multiple of the 8 XCDs; Hkv = 16 with 16-token chunks (one partial block,
+    the second wave group idle); three query groups at G = 8; against the oracle's partials."""
+    _prefix_partials_vs_oracle(B, Lp, chunk_tokens, 1.0, Hq, Hkv)
+
+
+def _prefix_partials_vs_oracle(B, Lp, chunk_tokens, scale, Hq, Hkv):
     import torch
     import _gpu
     import pdattn
-    print(f"[case] prefix kernel B={B} Lp={Lp} chunk_tokens={chunk_tokens} scale={scale}", flush=True)
-    bt = inputs.make_shared_prefix_batch(Lp, [16] * B, 32, 8, seed=30 + B)
+    print(f"[case] prefix kernel B={B} Lp={Lp} chunk_tokens={chunk_tokens} scale={scale} Hq={Hq} Hkv={Hkv}",
+          flush=True)
+    bt = inputs.make_shared_prefix_batch(Lp, [16] * B, Hq, Hkv, seed=30 + B)
     db = _gpu.DeviceBatch(bt)
     nchunks = (Lp + chunk_tokens - 1) // chunk_tokens
     rows = bt.B * bt.Hq
