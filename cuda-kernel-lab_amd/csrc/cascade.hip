@@ -59,7 +59,9 @@ __device__ __forceinline__ void ks_barrier() {
 
 // 16 bytes per lane from global memory into LDS: lane i's bytes land at lds + 16 i (M0 holds the
 // LDS address; one wait state between the M0 write and the load). The compiler does not count
-// these loads: the waits below are explicit.
+// these loads: the waits below are explicit. M0 is a reserved register to the compiler (hipcc
+// warns that a clobber of it is not preserved); on gfx950 nothing else in these kernels reads or
+// writes it, which the build lint checks on the assembly.
 __device__ __forceinline__ void ks_dma(const uint8_t* src, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                  :: "v"(src), "s"(lds) : "memory", "m0");

@@ -5,6 +5,10 @@
   null), and calls would also cost registers and latency in the hot loop.
 * No packed-FP32 instructions are emitted (the build disables them).
 * No kernel spills registers to scratch.
+* M0 is written only by the key-split prefix kernel's direct global->LDS loads (cascade.hip
+  issues them from inline asm that sets M0 and declares it clobbered): every M0 reference is
+  such a write, followed by the wait state and the load, so no compiler-generated code holds a
+  value in M0 across them.
 
 Every .hip source of the library is checked.
 """
@@ -57,3 +61,16 @@ def test_no_scratch_spills(name, tmp_path):
         assert names
     for n, sp, ss in zip(names, spills, sspills):
         assert int(sp) == 0 and int(ss) == 0, f"{name}.hip: {n} spills {sp} VGPRs, {ss} SGPRs"
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
+def test_m0_only_for_direct_lds_loads(tmp_path):
+    asm = _asm("cascade", tmp_path)
+    lines = [ln.split(";")[0].strip() for ln in asm.splitlines()]
+    lines = [ln for ln in lines if ln]
+    uses = [i for i, ln in enumerate(lines) if re.search(r"\bm0\b", ln)]
+    loads = sum(1 for ln in lines if ln.startswith("global_load_lds_dwordx4"))
+    assert uses and len(uses) == loads
+    for i in uses:
+        assert re.fullmatch(r"s_mov_b32 m0, s\d+", lines[i]), lines[i]
+        assert lines[i + 1] == "s_nop 0" and lines[i + 2].startswith("global_load_lds_dwordx4"), lines[i:i + 3]
