@@ -118,11 +118,13 @@ def test_prefix_kernel_full_query_groups(B, Lp, chunk_tokens, scale):
 def test_prefix_key_split_head_layouts(Hq, Hkv, B, Lp, chunk_tokens):
     """The key-split body at other head layouts: G = 8; Hkv = 2, whose grid width (query groups x
     kv heads = 4) is not a multiple of the 8 XCDs; Hkv = 16 with 16-token chunks (one partial block,
-    the second wave group idle); three query groups at G = 8; against the oracle's partials."""
-    _prefix_partials_vs_oracle(B, Lp, chunk_tokens, 1.0, Hq, Hkv)
+    the second wave group idle); three query groups at G = 8; partial rows two columns wider than
+    the chunks (part_stride = chunks + 2, the untouched columns must stay as they were); against the
+    oracle's partials."""
+    _prefix_partials_vs_oracle(B, Lp, chunk_tokens, 1.0, Hq, Hkv, pad=2)
 
 
-def _prefix_partials_vs_oracle(B, Lp, chunk_tokens, scale, Hq, Hkv):
+def _prefix_partials_vs_oracle(B, Lp, chunk_tokens, scale, Hq, Hkv, pad=0):
     import torch
     import _gpu
     import pdattn
@@ -133,17 +135,21 @@ def _prefix_partials_vs_oracle(B, Lp, chunk_tokens, scale, Hq, Hkv):
     nchunks = (Lp + chunk_tokens - 1) // chunk_tokens
     rows = bt.B * bt.Hq
     d = torch.device("cuda:0")
-    po = torch.full((rows, nchunks, 128), float("nan"), dtype=torch.float32, device=d)
-    pl = torch.full((rows, nchunks), float("nan"), dtype=torch.float32, device=d)
+    po = torch.full((rows, nchunks + pad, 128), float("nan"), dtype=torch.float32, device=d)
+    pl = torch.full((rows, nchunks + pad), float("nan"), dtype=torch.float32, device=d)
     pp = pdattn.PrefixParams()
     pp.q, pp.k_cache, pp.v_cache = db.q.data_ptr(), db.k.data_ptr(), db.v.data_ptr()
     pp.prefix_pages = db.indices.data_ptr()
     pp.part_o, pp.part_lse = po.data_ptr(), pl.data_ptr()
     pp.B, pp.Hq, pp.Hkv = bt.B, bt.Hq, bt.Hkv
-    pp.prefix_len, pp.chunk_tokens, pp.part_stride = Lp, chunk_tokens, nchunks
+    pp.prefix_len, pp.chunk_tokens, pp.part_stride = Lp, chunk_tokens, nchunks + pad
     pp.sm_scale = scale / np.sqrt(128)
     pdattn.cascade_prefix(pp)
     torch.cuda.synchronize()
+    if pad:
+        assert torch.isnan(po[:, nchunks:]).all() and torch.isnan(pl[:, nchunks:]).all(), \
+            "columns past the chunks were written"
+        po, pl = po[:, :nchunks], pl[:, :nchunks]
     indptr = np.arange(bt.B + 1, dtype=np.int32) * (Lp // 16)
     indices = np.concatenate([bt.indices[bt.indptr[b]:bt.indptr[b] + Lp // 16] for b in range(bt.B)])
     last = np.full(bt.B, 16, np.int32)
