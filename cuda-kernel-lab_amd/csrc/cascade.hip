@@ -332,11 +332,15 @@ __device__ __forceinline__ void prefix_chunk_ks(const PrefixArgs& a, KSSmem& sm,
             s[tq][1] = __builtin_bit_cast(pf32x4, pb[1]);
         }
     };
+    // The VALU phase sets each step's pace (a lone wave issues VALU work at about half the SIMD's
+    // rate), so the wave in it takes issue priority over its SIMD partner in the MFMA phase.
     auto valu_phase = [&](int m) {
+        __builtin_amdgcn_s_setprio(2);
         if (m < nfg)
             softmax(m, std::false_type{});
         else
             softmax(m, std::true_type{});
+        __builtin_amdgcn_s_setprio(0);
     };
     // Block loads of step i, issued after the barrier that starts it: K of block i + 1 (its buffer's
     // last reader, the scores of block i - 1, ran in step i - 1) and V of block i (the PV product of
